@@ -1,0 +1,96 @@
+// Device helpers for the CDNA4 (gfx950) kernels: f16 vectors, DPP row
+// reductions and the raw exp2 instruction.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+namespace dev {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float f16_to_f32(uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// Round-to-nearest-even f32 -> f16 (v_cvt_f16_f32 rounds by the mode
+// register, which HIP leaves at RNE).
+__device__ __forceinline__ uint16_t f32_to_f16(float value) {
+  return __builtin_bit_cast(uint16_t, (_Float16)value);
+}
+
+// v_exp_f32: 2^x, exact at 0, 0 at -inf.
+__device__ __forceinline__ float exp2_raw(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                         0xf, 0xf, false));
+}
+
+// DPP controls: quad_perm xor-1 / xor-2, row rotate by 4 / 8 within the
+// 16-lane row.
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+
+// Sum over each aligned group of N lanes (N a power of two <= 64); every
+// lane of the group receives the total.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_f32<kDppQuadXor1>(x);
+  if constexpr (N >= 4) x += dpp_f32<kDppQuadXor2>(x);
+  if constexpr (N >= 8) x += __shfl_xor(x, 4, 64);
+  if constexpr (N >= 16) x += __shfl_xor(x, 8, 64);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+// 16-lane row sum using only DPP (rotations make every lane hold the
+// total, as for group_sum<16>).
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<kDppQuadXor1>(x);
+  x += dpp_f32<kDppQuadXor2>(x);
+  x += dpp_f32<kDppRowRor4>(x);
+  x += dpp_f32<kDppRowRor8>(x);
+  return x;
+}
+
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float x) {
+  if constexpr (N == 16) {
+    return row16_sum(x);
+  } else if constexpr (N == 32) {
+    x = row16_sum(x);
+    return x + __shfl_xor(x, 16, 64);
+  } else {
+    return group_sum<N>(x);
+  }
+}
+
+// f16x2 dot product accumulated in f32 (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(fp16x2_t, a),
+                                __builtin_bit_cast(fp16x2_t, b), c, false);
+}
+
+__device__ __forceinline__ float lo_f16(uint32_t packed) {
+  return (float)__builtin_bit_cast(half2_t, packed).x;
+}
+__device__ __forceinline__ float hi_f16(uint32_t packed) {
+  return (float)__builtin_bit_cast(half2_t, packed).y;
+}
+
+}  // namespace dev
+}  // namespace mi

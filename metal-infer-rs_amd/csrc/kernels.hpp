@@ -1,0 +1,118 @@
+// Kernel parameter blocks and launchers shared by the host runtime and the
+// HIP kernels. All strides are in elements; every tensor the fast kernels
+// read has a unit innermost stride.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+namespace kernels {
+
+// Split-K "rows" attention: one workgroup per (sequence*token, KV head,
+// head chunk, key split). Serves Tiled, DecodeSplitKv, FlashDecode and the
+// batched decode. Q/O are [B, T, Hq, D]; K/V are [B, L, Hkv, D] views.
+struct RowsParams {
+  const uint16_t *q;
+  int64_t q_seq, q_tok, q_head;
+  const uint16_t *k;
+  int64_t k_seq, k_pos, k_head;
+  const uint16_t *v;
+  int64_t v_seq, v_pos, v_head;
+  uint16_t *out;
+  int64_t o_seq, o_tok, o_head;
+  float *partial;           // [units][max_splits][chunk][D + 2] f32
+  uint32_t *counters;       // [units] arrival counters, zero between calls
+  const uint32_t *lengths;  // per-sequence KV length, or null
+  uint32_t batch;           // B
+  uint32_t tokens;          // T
+  uint32_t q_heads, kv_heads, group;
+  uint32_t head_chunks;     // group / chunk
+  uint32_t kv_length;       // L (upper bound when lengths != null)
+  uint32_t causal;
+  uint32_t query_offset;    // ignored when lengths != null
+  uint32_t block_keys;      // keys per split
+  uint32_t max_splits;
+  float scale_log2;         // rsqrt(D) * log2(e)
+};
+
+// Exact two-pass attention (AttentionKind::Reference).
+struct NaiveParams {
+  const uint16_t *q;
+  int64_t q_tok, q_head;
+  const uint16_t *k;
+  int64_t k_pos, k_head;
+  const uint16_t *v;
+  int64_t v_pos, v_head;
+  uint16_t *out;
+  int64_t o_tok, o_head;
+  float *scores;            // [row_count][L] f32 when scores spill from LDS
+  uint32_t tokens, q_heads, kv_heads, head_dim, kv_length, causal,
+      query_offset;
+  float scale;              // rsqrt(D)
+};
+
+// KV append: source [T, H, D] -> cache [C, H, D] at `offset`.
+struct CopyKvParams {
+  const uint16_t *src;
+  int64_t s_tok, s_head;
+  uint16_t *dst;
+  int64_t d_pos, d_head;
+  uint32_t tokens, heads, head_dim, offset;
+};
+
+// Fused per-head RMSNorm + RoPE, K written into the cache.
+struct QkNormRopeParams {
+  const uint16_t *q;
+  int64_t q_tok, q_head;
+  const uint16_t *k;
+  int64_t k_tok, k_head;
+  const uint16_t *q_weight;
+  const uint16_t *k_weight;
+  uint16_t *q_out;
+  int64_t qo_tok, qo_head;
+  uint16_t *cache;
+  int64_t c_pos, c_head;
+  uint32_t tokens, q_heads, kv_heads, head_dim, offset;
+  float theta, epsilon;
+};
+
+// MFMA flash prefill (FlashPrefill at head_dim 128 / 64).
+struct PrefillParams {
+  const uint16_t *q;
+  int64_t q_tok, q_head;
+  const uint16_t *k;
+  int64_t k_pos, k_head;
+  const uint16_t *v;
+  int64_t v_pos, v_head;
+  uint16_t *out;
+  int64_t o_tok, o_head;
+  uint32_t tokens, q_heads, kv_heads, group, kv_length, causal, query_offset;
+  uint32_t row_tiles;       // ceil(T * group / BLOCK_M)
+  float scale_log2;
+};
+
+hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
+                       uint32_t chunk, hipStream_t stream);
+// Largest head chunk (of 8, 4, 2, 1) that divides `group`.
+uint32_t rows_chunk(uint32_t group);
+
+// Runs rows [row_begin, row_begin + row_count) of the flattened
+// (token, head) grid. Scores of up to kNaiveLdsKeys keys live in LDS; longer
+// rows spill to NaiveParams::scores, which must hold row_count * L floats.
+hipError_t launch_naive(const NaiveParams &p, uint32_t row_begin,
+                        uint32_t row_count, hipStream_t stream);
+constexpr uint32_t kNaiveLdsKeys = 12288;
+
+hipError_t launch_copy_kv(const CopyKvParams &p, hipStream_t stream);
+hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, hipStream_t stream);
+
+// Rows of the packed (token, head-in-group) M dimension per prefill
+// workgroup.
+constexpr uint32_t kPrefillBlockM = 128;
+bool prefill_supported(uint32_t head_dim);
+hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim,
+                          hipStream_t stream);
+
+}  // namespace kernels
+}  // namespace mi

@@ -1,0 +1,580 @@
+// Attention and KV-cache operations of the C ABI. Validation order and
+// error text follow crates/metal-infer-core/src/ops.rs (attention
+// :1050-1247, copy_into_cache :1249-1285, qk_norm_rope_cache :917-977);
+// the kernel choice is MI355X-specific.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mi {
+namespace {
+
+enum class Family { Naive, Rows, Prefill };
+
+struct AttnPlan {
+  Family family = Family::Rows;
+  uint32_t T = 0, Hq = 0, Hkv = 0, D = 0, L = 0, G = 0;
+  uint32_t waves = 4, chunk = 1, block_keys = 0, splits = 1;
+  uint64_t units = 0;            // rows-kernel (row, KV head, chunk) units
+  uint64_t scratch_bytes = 0;
+  uint32_t grid[3] = {0, 0, 0};
+  uint32_t threads = 0;
+  const char *kernel = "";
+};
+
+constexpr uint32_t kU32Max = 0xffffffffu;
+
+bool pow2(uint64_t x) { return x != 0 && (x & (x - 1)) == 0; }
+
+mi_status to_u32(int64_t value, const char *label, uint32_t *out) {
+  if (value < 0 || (uint64_t)value > kU32Max)
+    return fail(MI_ERR_SHAPE, std::string(label) + " does not fit in u32");
+  *out = (uint32_t)value;
+  return MI_OK;
+}
+
+uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// Whether a rank-3 f16 view can feed the 128-bit-load kernels: unit
+// innermost stride, outer strides and base aligned to `vec` halves.
+bool vector_friendly(const mi_tensor &t, uint32_t vec) {
+  if (t.stride[t.rank - 1] != 1) return false;
+  for (int32_t i = 0; i < t.rank - 1; ++i)
+    if (t.stride[i] % vec != 0) return false;
+  return reinterpret_cast<uintptr_t>(t.data) % (vec * 2) == 0;
+}
+
+// Default split size: enough workgroups to cover every CU twice, at least
+// 32 keys per split, and whole 32-key steps.
+uint32_t default_block(const Context *ctx, uint64_t units, uint32_t keys) {
+  const uint64_t target = 2ull * std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1);
+  if (units >= target || keys <= 32) return std::max<uint32_t>(32, ((keys + 31) / 32) * 32);
+  const uint64_t splits = (target + units - 1) / units;
+  uint64_t block = (keys + splits - 1) / splits;
+  block = std::max<uint64_t>(64, ((block + 31) / 32) * 32);
+  return (uint32_t)block;
+}
+
+// FlashDecode (block, threads) for a length (context.rs:258-267): the tuned
+// table if any, else (64, 256) as in the reference.
+void flash_config_for_length(const Context *ctx, uint64_t length, uint32_t *block,
+                             uint32_t *threads) {
+  if (ctx != nullptr)
+    for (const auto &e : ctx->flash_decode)
+      if (length <= e.limit) {
+        *block = e.block_keys;
+        *threads = e.threads;
+        return;
+      }
+  *block = 64;
+  *threads = 256;
+}
+
+mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t max_keys,
+                    uint32_t block_keys, uint32_t threads) {
+  p->family = Family::Rows;
+  p->kernel = "attn_rows";
+  p->waves = threads == 128 ? 2 : 4;
+  p->threads = p->waves * 64;
+  p->chunk = kernels::rows_chunk(p->G);
+  const uint64_t units = batch * p->T * p->Hkv * (p->G / p->chunk);
+  p->units = units;
+  p->block_keys = block_keys != 0 ? block_keys : default_block(ctx, units, max_keys);
+  p->splits = std::max<uint32_t>(1, ceil_div(std::max<uint32_t>(max_keys, 1), p->block_keys));
+  p->scratch_bytes =
+      p->splits > 1 ? units * p->splits * p->chunk * (uint64_t)(p->D + 2) * sizeof(float) : 0;
+  if (batch * p->T > 0xffffu || (uint64_t)p->Hkv * (p->G / p->chunk) > 0xffffu)
+    return fail(MI_ERR_SHAPE, "attention grid exceeds the launch limits");
+  p->grid[0] = p->splits;
+  p->grid[1] = p->Hkv * (p->G / p->chunk);
+  p->grid[2] = (uint32_t)(batch * p->T);
+  return MI_OK;
+}
+
+mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor *k,
+                         const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                         uint32_t block_keys, uint32_t threads, bool flash_explicit,
+                         const mi_tensor *out, AttnPlan *plan) {
+  if (q == nullptr || k == nullptr || v == nullptr || config == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null tensor or config");
+  if (kind < MI_ATTN_REFERENCE || kind > MI_ATTN_FLASH_DECODE)
+    return fail(MI_ERR_INVALID_ARGUMENT, "unknown attention kind");
+  mi_status st;
+  if ((st = require_f16(q)) != MI_OK || (st = require_f16(k)) != MI_OK ||
+      (st = require_f16(v)) != MI_OK)
+    return st;
+  if (q->rank != 3) return fail(MI_ERR_SHAPE, "query must have rank 3");
+  if (k->rank != 3) return fail(MI_ERR_SHAPE, "key must have rank 3");
+  if (v->rank != 3) return fail(MI_ERR_SHAPE, "value must have rank 3");
+  const int64_t tokens = q->shape[0], kv_length = k->shape[0];
+  if (q->shape[1] != (int64_t)config->query_heads || q->shape[2] != (int64_t)config->head_dim ||
+      k->shape[1] != (int64_t)config->kv_heads || k->shape[2] != (int64_t)config->head_dim ||
+      v->shape[0] != kv_length || v->shape[1] != k->shape[1] || v->shape[2] != k->shape[2])
+    return fail(MI_ERR_SHAPE, "attention tensor shapes do not match config");
+  if (config->kv_heads == 0 || config->query_heads % config->kv_heads != 0)
+    return fail(MI_ERR_SHAPE, "query_heads must be divisible by kv_heads");
+  if (kind != MI_ATTN_REFERENCE && (!pow2(config->head_dim) || config->head_dim > 256))
+    return fail(MI_ERR_SHAPE, "tiled attention requires a power-of-two head_dim <= 256");
+  uint32_t flash_block = 0, flash_threads = 0;
+  if (kind == MI_ATTN_FLASH_DECODE) {
+    if (flash_explicit) {
+      flash_block = block_keys;
+      flash_threads = threads;
+    } else {
+      flash_config_for_length(ctx, (uint64_t)kv_length, &flash_block, &flash_threads);
+    }
+    if (flash_block != 32 && flash_block != 64 && flash_block != 128 && flash_block != 256)
+      return fail(MI_ERR_SHAPE, "flash decode block size must be 32, 64, 128, or 256");
+    if (flash_threads != 128 && flash_threads != 256)
+      return fail(MI_ERR_SHAPE, "flash decode threadgroup size must be 128 or 256");
+  }
+  if (out != nullptr) {
+    if ((st = require_f16(out)) != MI_OK) return st;
+    if (out->rank != 3 || out->shape[0] != q->shape[0] || out->shape[1] != q->shape[1] ||
+        out->shape[2] != q->shape[2])
+      return fail(MI_ERR_SHAPE, "attention output must have the query's shape");
+  }
+  AttnPlan p;
+  uint32_t causal = config->causal != 0 ? 1 : 0;
+  (void)causal;
+  if ((st = to_u32(tokens, "tokens", &p.T)) != MI_OK) return st;
+  if ((st = to_u32(kv_length, "kv_length", &p.L)) != MI_OK) return st;
+  p.Hq = config->query_heads;
+  p.Hkv = config->kv_heads;
+  p.D = config->head_dim;
+  p.G = p.Hq / p.Hkv;
+  if ((kind == MI_ATTN_DECODE_SPLIT_KV || kind == MI_ATTN_FLASH_DECODE) && tokens != 1)
+    return fail(MI_ERR_SHAPE, "decode attention requires exactly one query token");
+  // The reference rejects FlashDecode unless Hq == 2 * Hkv (ops.rs:1141);
+  // the rows kernel serves every ratio, so that check is lifted.
+  const uint64_t window = (uint64_t)config->query_offset + 1;
+  const uint32_t available_last =
+      config->causal != 0 ? (uint32_t)std::min<uint64_t>(p.L, window + p.T - 1) : p.L;
+  if (kind == MI_ATTN_FLASH_DECODE && available_last == 0)
+    return fail(MI_ERR_SHAPE, "flash decode requires at least one available key");
+
+  const uint32_t vec = std::min<uint32_t>(8, p.D);
+  const bool vectorized = vector_friendly(*q, vec) && vector_friendly(*k, vec) &&
+                          vector_friendly(*v, vec) &&
+                          (out == nullptr || vector_friendly(*out, 1));
+  if (kind == MI_ATTN_REFERENCE || !vectorized) {
+    p.family = Family::Naive;
+    p.kernel = "attn_naive";
+    p.threads = 256;
+    p.grid[0] = p.T * p.Hq;
+    p.grid[1] = p.grid[2] = 1;
+    if (p.L > kernels::kNaiveLdsKeys)
+      p.scratch_bytes = (uint64_t)std::min<uint64_t>(p.grid[0], 4096) * p.L * sizeof(float);
+    *plan = p;
+    return MI_OK;
+  }
+  if (kind == MI_ATTN_FLASH_PREFILL && kernels::prefill_supported(p.D) &&
+      vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8)) {
+    p.family = Family::Prefill;
+    p.kernel = "attn_prefill";
+    p.threads = 256;
+    p.grid[0] = ceil_div((uint64_t)p.T * p.G, kernels::kPrefillBlockM);
+    p.grid[1] = p.Hkv;
+    p.grid[2] = 1;
+    *plan = p;
+    return MI_OK;
+  }
+  const uint32_t rows_block = kind == MI_ATTN_FLASH_DECODE ? flash_block : 0;
+  const uint32_t rows_threads = kind == MI_ATTN_FLASH_DECODE ? flash_threads : 256;
+  st = plan_rows(ctx, &p, 1, available_last, rows_block, rows_threads);
+  if (st != MI_OK) return st;
+  *plan = p;
+  return MI_OK;
+}
+
+void fill_info(const AttnPlan &p, mi_attention_plan_info *info) {
+  std::memset(info, 0, sizeof *info);
+  std::snprintf(info->kernel, sizeof info->kernel, "%s", p.kernel);
+  for (int i = 0; i < 3; ++i) info->grid[i] = p.grid[i];
+  info->block_threads = p.threads;
+  info->block_keys = p.family == Family::Rows ? p.block_keys : 0;
+  info->splits = p.family == Family::Rows ? p.splits : 1;
+  info->scratch_bytes = p.scratch_bytes;
+}
+
+mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
+  Context *ctx = batch->ctx;
+  void *scratch = nullptr;
+  mi_status st;
+  if (p.splits > 1) {
+    if ((st = ensure_counters(ctx, p.units)) != MI_OK) return st;
+    if ((st = scratch_alloc(batch, p.scratch_bytes, &scratch)) != MI_OK) return st;
+  }
+  rp.partial = static_cast<float *>(scratch);
+  rp.counters = ctx->counters;
+  rp.block_keys = p.block_keys;
+  rp.max_splits = p.splits;
+  rp.head_chunks = p.G / p.chunk;
+  rp.group = p.G;
+  st = launch(batch, p.kernel, [&](hipStream_t s) {
+    return kernels::launch_rows(rp, p.D, p.waves, p.chunk, s);
+  });
+  // In-order execution makes the range reusable by later work of the batch.
+  if (scratch != nullptr) scratch_free(ctx, scratch);
+  return st;
+}
+
+mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
+                        const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                        uint32_t block_keys, uint32_t threads, bool flash_explicit,
+                        const mi_tensor *out) {
+  if (batch == nullptr || out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch or output");
+  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  AttnPlan p;
+  mi_status st = plan_attention(batch->ctx, q, k, v, config, kind, block_keys, threads,
+                                flash_explicit, out, &p);
+  if (st != MI_OK) return st;
+  const float scale = 1.0f / std::sqrt((float)p.D);
+  const float log2e = 1.4426950408889634f;
+  auto qd = static_cast<const uint16_t *>(q->data);
+  auto kd = static_cast<const uint16_t *>(k->data);
+  auto vd = static_cast<const uint16_t *>(v->data);
+  auto od = static_cast<uint16_t *>(out->data);
+  if (p.family == Family::Naive) {
+    kernels::NaiveParams np{};
+    np.q = qd, np.q_tok = q->stride[0], np.q_head = q->stride[1];
+    np.k = kd, np.k_pos = k->stride[0], np.k_head = k->stride[1];
+    np.v = vd, np.v_pos = v->stride[0], np.v_head = v->stride[1];
+    np.out = od, np.o_tok = out->stride[0], np.o_head = out->stride[1];
+    np.tokens = p.T, np.q_heads = p.Hq, np.kv_heads = p.Hkv, np.head_dim = p.D;
+    np.kv_length = p.L, np.causal = config->causal != 0, np.query_offset = config->query_offset;
+    np.scale = scale;
+    if (q->stride[2] != 1 || k->stride[2] != 1 || v->stride[2] != 1 || out->stride[2] != 1)
+      return fail(MI_ERR_SHAPE, "attention tensors need a unit innermost stride");
+    const uint32_t rows = p.T * p.Hq;
+    uint32_t chunk_rows = rows;
+    void *scores = nullptr;
+    if (p.L > kernels::kNaiveLdsKeys) {
+      chunk_rows = (uint32_t)(p.scratch_bytes / ((uint64_t)p.L * sizeof(float)));
+      if ((st = scratch_alloc(batch, p.scratch_bytes, &scores)) != MI_OK) return st;
+      np.scores = static_cast<float *>(scores);
+    }
+    for (uint32_t begin = 0; begin < rows && st == MI_OK; begin += chunk_rows) {
+      const uint32_t count = std::min(chunk_rows, rows - begin);
+      st = launch(batch, p.kernel,
+                  [&](hipStream_t s) { return kernels::launch_naive(np, begin, count, s); });
+    }
+    if (scores != nullptr) scratch_free(batch->ctx, scores);
+    return st;
+  }
+  if (p.family == Family::Prefill) {
+    kernels::PrefillParams pp{};
+    pp.q = qd, pp.q_tok = q->stride[0], pp.q_head = q->stride[1];
+    pp.k = kd, pp.k_pos = k->stride[0], pp.k_head = k->stride[1];
+    pp.v = vd, pp.v_pos = v->stride[0], pp.v_head = v->stride[1];
+    pp.out = od, pp.o_tok = out->stride[0], pp.o_head = out->stride[1];
+    pp.tokens = p.T, pp.q_heads = p.Hq, pp.kv_heads = p.Hkv, pp.group = p.G;
+    pp.kv_length = p.L, pp.causal = config->causal != 0, pp.query_offset = config->query_offset;
+    pp.row_tiles = p.grid[0];
+    pp.scale_log2 = scale * log2e;
+    return launch(batch, p.kernel,
+                  [&](hipStream_t s) { return kernels::launch_prefill(pp, p.D, s); });
+  }
+  kernels::RowsParams rp{};
+  rp.q = qd, rp.q_seq = 0, rp.q_tok = q->stride[0], rp.q_head = q->stride[1];
+  rp.k = kd, rp.k_seq = 0, rp.k_pos = k->stride[0], rp.k_head = k->stride[1];
+  rp.v = vd, rp.v_seq = 0, rp.v_pos = v->stride[0], rp.v_head = v->stride[1];
+  rp.out = od, rp.o_seq = 0, rp.o_tok = out->stride[0], rp.o_head = out->stride[1];
+  rp.lengths = nullptr;
+  rp.batch = 1, rp.tokens = p.T, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+  rp.kv_length = p.L, rp.causal = config->causal != 0, rp.query_offset = config->query_offset;
+  rp.scale_log2 = scale * log2e;
+  return run_rows(batch, p, rp);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+mi_status mi_attention(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                       const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                       const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, kind, 0, 0, false, out);
+}
+
+mi_status mi_attention_flash_decode_with_block(mi_batch *batch, const mi_tensor *q,
+                                               const mi_tensor *k, const mi_tensor *v,
+                                               const mi_attention_config *config,
+                                               uint32_t block_keys, const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, 256, true, out);
+}
+
+mi_status mi_attention_flash_decode_with_configuration(
+    mi_batch *batch, const mi_tensor *q, const mi_tensor *k, const mi_tensor *v,
+    const mi_attention_config *config, uint32_t block_keys, uint32_t threads,
+    const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, threads, true,
+                       out);
+}
+
+mi_status mi_attention_plan(const mi_context *ctx, const mi_tensor *q, const mi_tensor *k,
+                            const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                            uint32_t block_keys, uint32_t threads,
+                            mi_attention_plan_info *info) {
+  if (info == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null plan output");
+  AttnPlan p;
+  const bool explicit_flash = block_keys != 0 || threads != 0;
+  mi_status st = plan_attention(ctx, q, k, v, config, kind, block_keys, threads,
+                                explicit_flash, nullptr, &p);
+  if (st != MI_OK) return st;
+  fill_info(p, info);
+  return MI_OK;
+}
+
+mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                                      const mi_tensor *v, const mi_tensor *lengths,
+                                      const mi_attention_config *config, uint32_t block_keys,
+                                      const mi_tensor *out) {
+  if (batch == nullptr || q == nullptr || k == nullptr || v == nullptr || lengths == nullptr ||
+      config == nullptr || out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
+  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  mi_status st;
+  if ((st = require_f16(q)) != MI_OK || (st = require_f16(k)) != MI_OK ||
+      (st = require_f16(v)) != MI_OK || (st = require_f16(out)) != MI_OK)
+    return st;
+  if (lengths->dtype != MI_U32)
+    return fail(MI_ERR_DTYPE, std::string("unsupported dtype: expected u32, got ") +
+                                  dtype_name(lengths->dtype));
+  if (q->rank != 3) return fail(MI_ERR_SHAPE, "query must have rank 3");
+  if (k->rank != 4 || v->rank != 4) return fail(MI_ERR_SHAPE, "batched KV must have rank 4");
+  if (lengths->rank != 1) return fail(MI_ERR_SHAPE, "lengths must have rank 1");
+  const int64_t B = q->shape[0], C = k->shape[1];
+  if (q->shape[1] != (int64_t)config->query_heads || q->shape[2] != (int64_t)config->head_dim ||
+      k->shape[0] != B || k->shape[2] != (int64_t)config->kv_heads ||
+      k->shape[3] != (int64_t)config->head_dim || v->shape[0] != B || v->shape[1] != C ||
+      v->shape[2] != k->shape[2] || v->shape[3] != k->shape[3] || lengths->shape[0] != B ||
+      out->rank != 3 || out->shape[0] != B || out->shape[1] != q->shape[1] ||
+      out->shape[2] != q->shape[2])
+    return fail(MI_ERR_SHAPE, "attention tensor shapes do not match config");
+  if (config->kv_heads == 0 || config->query_heads % config->kv_heads != 0)
+    return fail(MI_ERR_SHAPE, "query_heads must be divisible by kv_heads");
+  if (!pow2(config->head_dim) || config->head_dim > 256)
+    return fail(MI_ERR_SHAPE, "tiled attention requires a power-of-two head_dim <= 256");
+  const uint32_t vec = std::min<uint32_t>(8, config->head_dim);
+  if (!vector_friendly(*q, vec) || !vector_friendly(*k, vec) || !vector_friendly(*v, vec) ||
+      !vector_friendly(*out, 1))
+    return fail(MI_ERR_SHAPE, "batched decode needs unit-stride, vector-aligned rows");
+  AttnPlan p;
+  if ((st = to_u32(B, "batch", &p.T)) != MI_OK) return st;
+  if ((st = to_u32(C, "kv capacity", &p.L)) != MI_OK) return st;
+  p.T = 1;
+  p.Hq = config->query_heads, p.Hkv = config->kv_heads, p.D = config->head_dim;
+  p.G = p.Hq / p.Hkv;
+  if (block_keys == 0) block_keys = std::min<uint32_t>(512, std::max<uint32_t>(64, p.L));
+  if ((st = plan_rows(batch->ctx, &p, (uint64_t)B, p.L, block_keys, 256)) != MI_OK) return st;
+  kernels::RowsParams rp{};
+  rp.q = static_cast<const uint16_t *>(q->data);
+  rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
+  rp.k = static_cast<const uint16_t *>(k->data);
+  rp.k_seq = k->stride[0], rp.k_pos = k->stride[1], rp.k_head = k->stride[2];
+  rp.v = static_cast<const uint16_t *>(v->data);
+  rp.v_seq = v->stride[0], rp.v_pos = v->stride[1], rp.v_head = v->stride[2];
+  rp.out = static_cast<uint16_t *>(out->data);
+  rp.o_seq = out->stride[0], rp.o_tok = 0, rp.o_head = out->stride[1];
+  rp.lengths = static_cast<const uint32_t *>(lengths->data);
+  rp.batch = (uint32_t)B, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+  rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
+  rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
+  p.kernel = "attn_rows_batched";
+  return run_rows(batch, p, rp);
+}
+
+mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx, uint64_t length,
+                                                   uint32_t *block_keys, uint32_t *threads) {
+  if (block_keys == nullptr || threads == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null output");
+  flash_config_for_length(ctx, length, block_keys, threads);
+  return MI_OK;
+}
+
+mi_status mi_tune_flash_decode(mi_context *ctx, uint32_t query_heads, uint32_t kv_heads,
+                               uint32_t head_dim) {
+  if (ctx == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null context");
+  if (kv_heads == 0 || head_dim == 0 || query_heads % kv_heads != 0 || !pow2(head_dim) ||
+      head_dim > 256)
+    return MI_OK;  // nothing to tune, as the reference's early return
+  using clock = std::chrono::steady_clock;
+  const auto started = clock::now();
+  const auto budget = std::chrono::seconds(2);
+  const uint64_t lengths[] = {512, 640, 1024, 2048, 4096, 8192};
+  const uint64_t maximum = 8192;
+  const uint32_t candidates[8][2] = {{64, 256}, {32, 256},  {128, 256}, {256, 256},
+                                     {64, 128}, {32, 128}, {128, 128}, {256, 128}};
+  int64_t qshape[3] = {1, query_heads, head_dim};
+  int64_t cshape[3] = {(int64_t)maximum, kv_heads, head_dim};
+  mi_tensor q, key, value, out;
+  mi_status st;
+  if ((st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &q)) != MI_OK) return st;
+  if ((st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &key)) != MI_OK) return st;
+  if ((st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &value)) != MI_OK) return st;
+  if ((st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &out)) != MI_OK) return st;
+  // 1.0 queries and 0.5 cache entries (context.rs:282-287).
+  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(q.data), 0x3c00, element_count(q));
+  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(key.data), 0x3800, element_count(key));
+  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(value.data), 0x3800, element_count(value));
+  (void)hipDeviceSynchronize();
+  std::vector<FlashDecodeEntry> chosen;
+  for (uint64_t length : lengths) {
+    if (clock::now() - started >= budget) break;
+    mi_tensor k_prefix, v_prefix;
+    mi_tensor_prefix(&key, (int64_t)length, &k_prefix);
+    mi_tensor_prefix(&value, (int64_t)length, &v_prefix);
+    mi_attention_config cfg{query_heads, kv_heads, head_dim, 1, (uint32_t)(length - 1)};
+    uint64_t best_ns = UINT64_MAX;
+    uint32_t best_block = 64, best_threads = 256;
+    for (const auto &cand : candidates) {
+      if (clock::now() - started >= budget) break;
+      uint64_t samples[3];
+      bool ok = true;
+      for (auto &sample : samples) {
+        mi_batch *batch = nullptr;
+        mi_dispatch_stats stats{};
+        if (mi_batch_begin(ctx, &batch) != MI_OK) { ok = false; break; }
+        if (mi_attention_flash_decode_with_configuration(batch, &q, &k_prefix, &v_prefix, &cfg,
+                                                         cand[0], cand[1], &out) != MI_OK) {
+          mi_batch_abandon(batch);
+          ok = false;
+          break;
+        }
+        if (mi_batch_finish(batch, &stats) != MI_OK) { ok = false; break; }
+        sample = stats.gpu_ns;
+      }
+      if (!ok) continue;
+      std::sort(samples, samples + 3);
+      if (samples[1] < best_ns) {
+        best_ns = samples[1];
+        best_block = cand[0];
+        best_threads = cand[1];
+      }
+    }
+    chosen.push_back({length, best_block, best_threads});
+  }
+  mi_tensor_free(ctx, &q);
+  mi_tensor_free(ctx, &key);
+  mi_tensor_free(ctx, &value);
+  mi_tensor_free(ctx, &out);
+  ctx->flash_decode = chosen;
+  clear_error();
+  return MI_OK;
+}
+
+int32_t mi_attention_kind_for_tokens(int32_t configured, uint64_t tokens, uint64_t active_length,
+                                     uint64_t query_heads_per_kv) {
+  // qwen3.rs:799-822 with the G == 2 condition lifted: the split-K kernel is
+  // ratio-generic, so long single-token decodes take FlashDecode for every
+  // GQA ratio.
+  (void)query_heads_per_kv;
+  switch (configured) {
+    case MI_ATTN_TILED:
+      if (tokens >= 32) return MI_ATTN_FLASH_PREFILL;
+      if (tokens == 1) return active_length >= 256 ? MI_ATTN_FLASH_DECODE : MI_ATTN_DECODE_SPLIT_KV;
+      return MI_ATTN_TILED;
+    case MI_ATTN_DECODE_SPLIT_KV:
+      return tokens == 1 ? MI_ATTN_DECODE_SPLIT_KV : MI_ATTN_TILED;
+    case MI_ATTN_FLASH_DECODE:
+      return tokens == 1 ? MI_ATTN_FLASH_DECODE : MI_ATTN_TILED;
+    case MI_ATTN_FLASH_PREFILL:
+      if (tokens == 1) return active_length >= 256 ? MI_ATTN_FLASH_DECODE : MI_ATTN_DECODE_SPLIT_KV;
+      return MI_ATTN_FLASH_PREFILL;
+    default:
+      return configured;
+  }
+}
+
+mi_status mi_copy_into_cache(mi_batch *batch, const mi_tensor *source, const mi_tensor *cache,
+                             uint64_t offset) {
+  if (batch == nullptr || source == nullptr || cache == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch or tensor");
+  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  mi_status st;
+  if ((st = require_f16(source)) != MI_OK || (st = require_f16(cache)) != MI_OK) return st;
+  if (source->rank != 3) return fail(MI_ERR_SHAPE, "KV source must have rank 3");
+  if (cache->rank != 3) return fail(MI_ERR_SHAPE, "KV cache must have rank 3");
+  if (source->shape[1] != cache->shape[1] || source->shape[2] != cache->shape[2])
+    return fail(MI_ERR_SHAPE, "KV source/cache shapes are incompatible");
+  if (offset + (uint64_t)source->shape[0] > (uint64_t)cache->shape[0])
+    return fail(MI_ERR_SHAPE, "KV cache capacity exceeded");
+  if (source->stride[2] != 1 || cache->stride[2] != 1)
+    return fail(MI_ERR_SHAPE, "KV rows need a unit innermost stride");
+  kernels::CopyKvParams cp{};
+  uint32_t tmp;
+  if ((st = to_u32(source->shape[0], "tokens", &cp.tokens)) != MI_OK) return st;
+  if ((st = to_u32((int64_t)offset, "offset", &cp.offset)) != MI_OK) return st;
+  if ((st = to_u32(source->shape[1] * source->shape[2], "stride", &tmp)) != MI_OK) return st;
+  cp.src = static_cast<const uint16_t *>(source->data);
+  cp.s_tok = source->stride[0], cp.s_head = source->stride[1];
+  cp.dst = static_cast<uint16_t *>(cache->data);
+  cp.d_pos = cache->stride[0], cp.d_head = cache->stride[1];
+  cp.heads = (uint32_t)source->shape[1];
+  cp.head_dim = (uint32_t)source->shape[2];
+  return launch(batch, "copy_kv", [&](hipStream_t s) { return kernels::launch_copy_kv(cp, s); });
+}
+
+mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                                const mi_tensor *q_weight, const mi_tensor *k_weight,
+                                const mi_tensor *key_cache,
+                                const mi_qk_norm_rope_cache_config *config,
+                                const mi_tensor *q_out) {
+  if (batch == nullptr || q == nullptr || k == nullptr || q_weight == nullptr ||
+      k_weight == nullptr || key_cache == nullptr || config == nullptr || q_out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
+  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  mi_status st;
+  if ((st = require_f16(q)) != MI_OK || (st = require_f16(k)) != MI_OK ||
+      (st = require_f16(q_weight)) != MI_OK || (st = require_f16(k_weight)) != MI_OK ||
+      (st = require_f16(key_cache)) != MI_OK)
+    return st;
+  if (q->rank != 3) return fail(MI_ERR_SHAPE, "query must have rank 3");
+  if (k->rank != 3) return fail(MI_ERR_SHAPE, "key must have rank 3");
+  if (key_cache->rank != 3) return fail(MI_ERR_SHAPE, "key cache must have rank 3");
+  const int64_t tokens = q->shape[0], head_dim = q->shape[2];
+  if (tokens != k->shape[0] || head_dim != k->shape[2] || k->shape[1] != key_cache->shape[1] ||
+      head_dim != key_cache->shape[2] || q_weight->rank != 1 || q_weight->shape[0] != head_dim ||
+      k_weight->rank != 1 || k_weight->shape[0] != head_dim)
+    return fail(MI_ERR_SHAPE, "Q/K transform tensor shapes are incompatible");
+  if (head_dim % 2 != 0 || (uint64_t)config->offset + (uint64_t)tokens > (uint64_t)key_cache->shape[0])
+    return fail(MI_ERR_SHAPE, "Q/K transform has invalid head_dim or cache offset");
+  if ((st = require_f16(q_out)) != MI_OK) return st;
+  if (q_out->rank != 3 || q_out->shape[0] != q->shape[0] || q_out->shape[1] != q->shape[1] ||
+      q_out->shape[2] != q->shape[2])
+    return fail(MI_ERR_SHAPE, "Q/K transform output must have the query's shape");
+  if (q->stride[2] != 1 || k->stride[2] != 1 || key_cache->stride[2] != 1 ||
+      q_out->stride[2] != 1 || q_weight->stride[0] != 1 || k_weight->stride[0] != 1)
+    return fail(MI_ERR_SHAPE, "Q/K transform tensors need a unit innermost stride");
+  kernels::QkNormRopeParams qp{};
+  if ((st = to_u32(tokens, "tokens", &qp.tokens)) != MI_OK) return st;
+  if ((st = to_u32(q->shape[1], "query heads", &qp.q_heads)) != MI_OK) return st;
+  if ((st = to_u32(k->shape[1], "KV heads", &qp.kv_heads)) != MI_OK) return st;
+  if ((st = to_u32(head_dim, "head dim", &qp.head_dim)) != MI_OK) return st;
+  qp.offset = config->offset;
+  qp.theta = config->theta;
+  qp.epsilon = config->epsilon;
+  qp.q = static_cast<const uint16_t *>(q->data), qp.q_tok = q->stride[0], qp.q_head = q->stride[1];
+  qp.k = static_cast<const uint16_t *>(k->data), qp.k_tok = k->stride[0], qp.k_head = k->stride[1];
+  qp.q_weight = static_cast<const uint16_t *>(q_weight->data);
+  qp.k_weight = static_cast<const uint16_t *>(k_weight->data);
+  qp.q_out = static_cast<uint16_t *>(q_out->data);
+  qp.qo_tok = q_out->stride[0], qp.qo_head = q_out->stride[1];
+  qp.cache = static_cast<uint16_t *>(key_cache->data);
+  qp.c_pos = key_cache->stride[0], qp.c_head = key_cache->stride[1];
+  return launch(batch, "qk_norm_rope_cache",
+                [&](hipStream_t s) { return kernels::launch_qk_norm_rope(qp, s); });
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// Host runtime behind the C ABI: context, device memory, scratch arenas,
+// batches and per-kernel profiling. Counterpart of
+// crates/metal-infer-core/src/context.rs, designed for HIP: one in-order
+// stream per context, device memory from hipMalloc, and HIP events for
+// batch and per-kernel GPU time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "mi_attn.h"
+
+namespace mi {
+
+// Records `message` as this thread's last error and returns `status`.
+mi_status fail(mi_status status, const std::string &message);
+mi_status hip_fail(mi_status status, const char *what, hipError_t err);
+void clear_error();
+const std::string &last_error_string();
+
+size_t dtype_size(int32_t dtype);
+const char *dtype_name(int32_t dtype);
+
+// One arena chunk: a device allocation with a sorted free list of
+// [start, end) byte ranges (context.rs:173-190).
+struct ScratchChunk {
+  void *base = nullptr;
+  size_t size = 0;
+  std::vector<std::pair<size_t, size_t>> free;
+};
+
+// A scratch arena; a batch holds one exclusively while it is in flight
+// (context.rs:715-729).
+struct ScratchPool {
+  std::vector<ScratchChunk> chunks;
+  bool busy = false;
+};
+
+struct Lease {
+  ScratchPool *pool;
+  size_t chunk;
+  size_t start;
+  size_t end;
+};
+
+// Arena chunks are at least this large (the reference uses 1 MiB chunks
+// for Metal's shared memory; split-K partials of a 32-sequence decode are
+// tens of MiB, so chunks start bigger here).
+constexpr size_t kScratchChunkBytes = 32ull << 20;
+constexpr size_t kScratchAlignment = 256;
+
+struct FlashDecodeEntry {
+  uint64_t limit;
+  uint32_t block_keys;
+  uint32_t threads;
+};
+
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name;
+  uint32_t compute_units = 0;
+  uint64_t allocated = 0;
+  std::vector<std::unique_ptr<ScratchPool>> pools;
+  std::unordered_map<uintptr_t, Lease> leases;
+  std::unordered_map<uintptr_t, size_t> tensors;  // mi_tensor_empty sizes
+  // Split-K arrival counters; zero between launches (the kernel's last
+  // workgroup resets its own counter).
+  uint32_t *counters = nullptr;
+  size_t counter_capacity = 0;
+  bool profiling = false;
+  std::vector<mi_kernel_profile> profiles;
+  std::vector<FlashDecodeEntry> flash_decode;  // tuned table, sorted
+};
+
+struct LaunchRecord {
+  std::string kernel;
+  hipEvent_t start;
+  hipEvent_t end;
+};
+
+struct Batch {
+  Context *ctx = nullptr;
+  ScratchPool *pool = nullptr;
+  hipEvent_t start = nullptr;
+  hipEvent_t end = nullptr;
+  bool committed = false;
+  std::chrono::steady_clock::time_point commit_time;
+  std::vector<LaunchRecord> launches;
+};
+
+// Leases `bytes` from the batch's arena (first fit, 256-B aligned).
+mi_status scratch_alloc(Batch *batch, size_t bytes, void **out);
+mi_status scratch_free(Context *ctx, void *ptr);
+
+// Ensures at least `count` zeroed arrival counters exist. Growing drains
+// the stream first, since in-flight kernels may hold the old buffer.
+mi_status ensure_counters(Context *ctx, size_t count);
+
+// Launches through `fn` on the batch stream, bracketed by HIP events when
+// kernel profiling is on. `fn` returns the launch's hipError_t.
+template <typename Fn>
+mi_status launch(Batch *batch, const char *kernel, Fn &&fn) {
+  hipEvent_t start = nullptr, end = nullptr;
+  if (batch->ctx->profiling) {
+    if (hipEventCreate(&start) != hipSuccess ||
+        hipEventCreate(&end) != hipSuccess)
+      return fail(MI_ERR_PROFILING, "could not create profiling events");
+    hipEventRecord(start, batch->ctx->stream);
+  }
+  hipError_t err = fn(batch->ctx->stream);
+  if (err != hipSuccess) {
+    if (start) hipEventDestroy(start);
+    if (end) hipEventDestroy(end);
+    return hip_fail(MI_ERR_PIPELINE, kernel, err);
+  }
+  if (start) {
+    hipEventRecord(end, batch->ctx->stream);
+    batch->launches.push_back({kernel, start, end});
+  }
+  return MI_OK;
+}
+
+// Tensor helpers.
+bool is_contiguous(const mi_tensor &t);
+uint64_t element_count(const mi_tensor &t);
+mi_status require_f16(const mi_tensor *t);
+
+}  // namespace mi
+
+// Opaque handle types of the C ABI.
+struct mi_context : mi::Context {};
+struct mi_batch : mi::Batch {};
+struct mi_kv_cache {
+  mi::Context *ctx = nullptr;
+  void *base = nullptr;
+  uint32_t layers = 0;
+  uint32_t kv_heads = 0;
+  uint32_t head_dim = 0;
+  uint64_t capacity = 0;
+  uint64_t filled = 0;
+};

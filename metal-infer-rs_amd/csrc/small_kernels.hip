@@ -1,0 +1,176 @@
+// The exact Reference attention, the KV-cache append and the fused
+// QK-RMSNorm + RoPE + K-append kernels.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mi {
+namespace kernels {
+namespace {
+
+using namespace mi::dev;
+
+// AttentionKind::Reference: the exact two-pass softmax of
+// attention_reference_f16 (transformer.metal:1579-1612), one workgroup per
+// (query token, query head). Each key's score is summed over x in
+// ascending order (one thread per key), pass 2 runs one thread per output
+// dimension over keys in ascending order, and contraction is off, so every
+// f32 operation is the one the reference's source spells out.
+__global__ __launch_bounds__(256) void attn_naive_kernel(NaiveParams p,
+                                                         uint32_t row_begin) {
+#pragma clang fp contract(off)
+  extern __shared__ float s_scores[];
+  __shared__ float s_red[256];
+  const uint32_t row = row_begin + blockIdx.x;
+  const uint32_t qi = row / p.q_heads;
+  const uint32_t h = row % p.q_heads;
+  const uint32_t kvh = h / (p.q_heads / p.kv_heads);
+  const uint64_t window = (uint64_t)p.query_offset + qi + 1;
+  const uint32_t available =
+      p.causal != 0 ? (uint32_t)min((uint64_t)p.kv_length, window)
+                    : p.kv_length;
+  float *scores = p.kv_length <= kNaiveLdsKeys
+                      ? s_scores
+                      : p.scores + (size_t)blockIdx.x * p.kv_length;
+  const uint16_t *q = p.q + (int64_t)qi * p.q_tok + (int64_t)h * p.q_head;
+  const uint16_t *k = p.k + (int64_t)kvh * p.k_head;
+  const uint16_t *v = p.v + (int64_t)kvh * p.v_head;
+
+  for (uint32_t j = threadIdx.x; j < available; j += blockDim.x) {
+    const uint16_t *kr = k + (int64_t)j * p.k_pos;
+    float score = 0.0f;
+    for (uint32_t x = 0; x < p.head_dim; ++x)
+      score += f16_to_f32(q[x]) * f16_to_f32(kr[x]);
+    scores[j] = score;
+  }
+  __syncthreads();
+  float local = -INFINITY;
+  for (uint32_t j = threadIdx.x; j < available; j += blockDim.x)
+    local = fmaxf(local, scores[j] * p.scale);
+  s_red[threadIdx.x] = local;
+  __syncthreads();
+  for (uint32_t stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+    if (threadIdx.x < stride)
+      s_red[threadIdx.x] =
+          fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + stride]);
+    __syncthreads();
+  }
+  const float maximum = s_red[0];
+  for (uint32_t d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
+    float denominator = 0.0f, numerator = 0.0f;
+    for (uint32_t j = 0; j < available; ++j) {
+      const float probability = expf(scores[j] * p.scale - maximum);
+      denominator += probability;
+      numerator += probability * f16_to_f32(v[(int64_t)j * p.v_pos + d]);
+    }
+    p.out[(int64_t)qi * p.o_tok + (int64_t)h * p.o_head + d] =
+        f32_to_f16(numerator / denominator);
+  }
+}
+
+// KV append (copy_kv_f16, transformer.metal:2318-2325) into any cache
+// layout: each thread moves 8 halves (16 B) when rows allow it.
+template <int VEC>
+__global__ __launch_bounds__(256) void copy_kv_kernel(CopyKvParams p) {
+  const uint32_t per_row = p.head_dim / VEC;
+  const uint64_t total = (uint64_t)p.tokens * p.heads * per_row;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+       i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t c = (uint32_t)(i % per_row);
+    const uint64_t r = i / per_row;
+    const uint32_t h = (uint32_t)(r % p.heads);
+    const uint32_t t = (uint32_t)(r / p.heads);
+    const uint16_t *src =
+        p.src + (int64_t)t * p.s_tok + (int64_t)h * p.s_head + c * VEC;
+    uint16_t *dst = p.dst + (int64_t)(p.offset + t) * p.d_pos +
+                    (int64_t)h * p.d_head + c * VEC;
+    if constexpr (VEC == 8) {
+      *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+}
+
+// qk_norm_rope_cache_f16 (transformer.metal:1533-1577): one wave per
+// (token, head) row; query rows first, then key rows, which are written
+// straight into the cache at position offset + token.
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(QkNormRopeParams p) {
+#pragma clang fp contract(off)
+  const uint32_t group = blockIdx.x;
+  const uint32_t query_rows = p.tokens * p.q_heads;
+  const bool is_query = group < query_rows;
+  const uint32_t row = is_query ? group : group - query_rows;
+  const uint32_t heads = is_query ? p.q_heads : p.kv_heads;
+  const uint32_t token = row / heads;
+  const uint32_t head = row % heads;
+  const uint16_t *input =
+      is_query ? p.q + (int64_t)token * p.q_tok + (int64_t)head * p.q_head
+               : p.k + (int64_t)token * p.k_tok + (int64_t)head * p.k_head;
+  const uint16_t *weight = is_query ? p.q_weight : p.k_weight;
+  uint16_t *output =
+      is_query
+          ? p.q_out + (int64_t)token * p.qo_tok + (int64_t)head * p.qo_head
+          : p.cache + (int64_t)(p.offset + token) * p.c_pos +
+                (int64_t)head * p.c_head;
+  const uint32_t lane = threadIdx.x;
+  float sum = 0.0f;
+  for (uint32_t i = lane; i < p.head_dim; i += 64) {
+    const float value = f16_to_f32(input[i]);
+    sum += value * value;
+  }
+  for (int mask = 32; mask > 0; mask >>= 1) sum += __shfl_xor(sum, mask, 64);
+  const float scale = 1.0f / sqrtf(sum / (float)p.head_dim + p.epsilon);
+  const uint32_t half = p.head_dim / 2;
+  for (uint32_t pair = lane; pair < half; pair += 64) {
+    const uint32_t second = pair + half;
+    const float x = f16_to_f32(input[pair]) * scale * f16_to_f32(weight[pair]);
+    const float y =
+        f16_to_f32(input[second]) * scale * f16_to_f32(weight[second]);
+    const float frequency =
+        powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
+    const float angle = (float)(token + p.offset) * frequency;
+    const float c = cosf(angle), s = sinf(angle);
+    output[pair] = f32_to_f16(x * c - y * s);
+    output[second] = f32_to_f16(x * s + y * c);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_naive(const NaiveParams &p, uint32_t row_begin,
+                        uint32_t row_count, hipStream_t stream) {
+  if (row_count == 0) return hipSuccess;
+  const size_t lds =
+      p.kv_length <= kNaiveLdsKeys ? (size_t)p.kv_length * sizeof(float) : 0;
+  attn_naive_kernel<<<row_count, 256, lds, stream>>>(p, row_begin);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_kv(const CopyKvParams &p, hipStream_t stream) {
+  const bool vec8 =
+      p.head_dim % 8 == 0 && p.s_tok % 8 == 0 && p.s_head % 8 == 0 &&
+      p.d_pos % 8 == 0 && p.d_head % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(p.src) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(p.dst) % 16 == 0;
+  const uint64_t items =
+      (uint64_t)p.tokens * p.heads * (vec8 ? p.head_dim / 8 : p.head_dim);
+  if (items == 0) return hipSuccess;
+  const uint64_t blocks64 = (items + 255) / 256;
+  const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
+  if (vec8)
+    copy_kv_kernel<8><<<blocks, 256, 0, stream>>>(p);
+  else
+    copy_kv_kernel<1><<<blocks, 256, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(const QkNormRopeParams &p,
+                               hipStream_t stream) {
+  const uint32_t groups = p.tokens * (p.q_heads + p.kv_heads);
+  if (groups == 0) return hipSuccess;
+  qk_norm_rope_kernel<<<groups, 64, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+}  // namespace kernels
+}  // namespace mi

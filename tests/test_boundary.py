@@ -1,0 +1,212 @@
+"""CPU tests of the C-ABI boundary: loading, exports, host-side validation.
+
+No GPU work happens here. mi_attention_plan runs the same validation and
+kernel choice as mi_attention without touching device memory, so every
+error path of ops.rs:1065-1150 is forced from the host.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import mi_attn
+from mi_attn import (DECODE_SPLIT_KV, FLASH_DECODE, FLASH_PREFILL, REFERENCE, TILED, F16, F32,
+                     AttentionConfig, MiError, describe)
+
+ROOT = Path(__file__).resolve().parent.parent
+FAKE = 0x7F0000000000  # 256-B aligned address; plan() never dereferences it
+
+
+def tensor(shape, dtype=F16, strides=None, offset=0):
+    return mi_attn.Tensor(describe(FAKE + offset, shape, strides, dtype))
+
+
+def plan(q, k, v, cfg, kind, block=0, threads=0):
+    return mi_attn.plan(q, k, v, cfg, kind, block, threads)
+
+
+def declared(header: str) -> list[str]:
+    text = (ROOT / "include" / header).read_text()
+    return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+def exported(lib: Path) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], check=True,
+                         capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+@pytest.mark.parametrize("header,lib", [("mi_attn.h", "libmi_attn.so"),
+                                        ("mi_bench.h", "libmi_bench.so")])
+def test_library_exports_every_declared_symbol(header, lib):
+    path = ROOT / "metal-infer-rs_amd" / lib
+    names = declared(header)
+    assert len(names) > 0
+    missing = set(names) - exported(path)
+    assert not missing, f"{lib} lacks {sorted(missing)}"
+    handle = ctypes.CDLL(str(path))
+    for name in names:
+        getattr(handle, name)
+
+
+def test_abi_version_and_status_names():
+    assert mi_attn.lib().mi_abi_version() == 1
+    assert mi_attn.lib().mi_status_name(8) == b"invalid tensor shape"
+    assert mi_attn.lib().mi_status_name(9) == b"unsupported dtype"
+
+
+def test_product_library_does_not_link_the_oracle():
+    out = subprocess.run(["ldd", str(ROOT / "metal-infer-rs_amd" / "libmi_attn.so")],
+                         capture_output=True, text=True).stdout
+    assert "oracle" not in out
+    assert "orc_" not in " ".join(exported(ROOT / "metal-infer-rs_amd" / "libmi_attn.so"))
+
+
+# ------------------------------------------- validation (ops.rs:1065-1150) --
+
+def _decode(hq=16, hkv=8, d=128, L=2048):
+    return (tensor((1, hq, d)), tensor((L, hkv, d)), tensor((L, hkv, d)),
+            AttentionConfig(hq, hkv, d, True, L - 1))
+
+
+def expect(status, fragment, fn, *args):
+    with pytest.raises(MiError) as err:
+        fn(*args)
+    assert err.value.name == status
+    assert fragment in err.value.message
+
+
+def test_dtype_and_rank_errors():
+    q, k, v, cfg = _decode()
+    expect("MI_ERR_DTYPE", "expected f16, got f32", plan, tensor((1, 16, 128), F32), k, v, cfg,
+           TILED)
+    expect("MI_ERR_SHAPE", "query must have rank 3", plan, tensor((16, 128)), k, v, cfg, TILED)
+    expect("MI_ERR_SHAPE", "key must have rank 3", plan, q, tensor((2048, 1024)), v, cfg, TILED)
+    expect("MI_ERR_SHAPE", "value must have rank 3", plan, q, k, tensor((2048, 1024)), cfg, TILED)
+
+
+def test_shape_config_and_ratio_errors():
+    q, k, v, cfg = _decode()
+    expect("MI_ERR_SHAPE", "do not match config", plan, q, k, v,
+           AttentionConfig(16, 4, 128, True, 0), TILED)
+    expect("MI_ERR_SHAPE", "do not match config", plan, q, k, tensor((2047, 8, 128)), cfg, TILED)
+    q3, k3 = tensor((1, 12, 128)), tensor((4, 8, 128))
+    expect("MI_ERR_SHAPE", "divisible by kv_heads", plan, q3, k3, k3,
+           AttentionConfig(12, 8, 128, True, 3), TILED)
+    expect("MI_ERR_SHAPE", "do not match config", plan, q3, k3, k3,
+           AttentionConfig(12, 0, 128, True, 3), TILED)
+
+
+def test_head_dim_rules():
+    q, k = tensor((2, 4, 96)), tensor((2, 2, 96))
+    cfg = AttentionConfig(4, 2, 96, True, 0)
+    expect("MI_ERR_SHAPE", "power-of-two head_dim <= 256", plan, q, k, k, cfg, FLASH_PREFILL)
+    assert plan(q, k, k, cfg, REFERENCE)["kernel"] == "attn_naive"  # Reference takes any D
+    q5, k5 = tensor((2, 4, 512)), tensor((2, 2, 512))
+    expect("MI_ERR_SHAPE", "power-of-two head_dim <= 256", plan, q5, k5, k5,
+           AttentionConfig(4, 2, 512, True, 0), TILED)
+
+
+def test_decode_kinds_need_one_token():
+    q, k = tensor((2, 2, 128)), tensor((8, 1, 128))
+    cfg = AttentionConfig(2, 1, 128, True, 6)
+    for kind in (DECODE_SPLIT_KV, FLASH_DECODE):
+        expect("MI_ERR_SHAPE", "exactly one query token", plan, q, k, k, cfg, kind)
+
+
+def test_flash_decode_configuration_is_validated():
+    q, k, v, cfg = _decode()
+    expect("MI_ERR_SHAPE", "block size must be 32, 64, 128, or 256", plan, q, k, v, cfg,
+           FLASH_DECODE, 48, 256)
+    expect("MI_ERR_SHAPE", "threadgroup size must be 128 or 256", plan, q, k, v, cfg,
+           FLASH_DECODE, 64, 64)
+    for block in (32, 64, 128, 256):
+        for threads in (128, 256):
+            p = plan(q, k, v, cfg, FLASH_DECODE, block, threads)
+            assert p["block_keys"] == block and p["block_threads"] == threads
+            assert p["splits"] == -(-2048 // block)
+    # default configuration (context.rs:258-267): (64, 256)
+    p = plan(q, k, v, cfg, FLASH_DECODE)
+    assert (p["block_keys"], p["block_threads"]) == (64, 256)
+
+
+def test_flash_decode_accepts_every_gqa_ratio():
+    # Deliberate extension: the reference requires Hq == 2 * Hkv (ops.rs:1141).
+    for hq, hkv in ((16, 8), (32, 8), (64, 8), (8, 8), (24, 8)):
+        q, k, v, cfg = _decode(hq, hkv)
+        p = plan(q, k, v, cfg, FLASH_DECODE)
+        assert p["kernel"] == "attn_rows"
+        assert p["grid"][1] * {16: 2, 32: 4, 64: 8, 8: 1, 24: 1}[hq] // max(
+            1, {16: 2, 32: 4, 64: 8, 8: 1, 24: 1}[hq]) >= hkv
+
+
+def test_causal_window_bounds_the_splits():
+    # Keys past query_offset are never visited: 65 keys, offset 62 -> 63 visible.
+    q, k, v = tensor((1, 16, 128)), tensor((65, 8, 128)), tensor((65, 8, 128))
+    p = plan(q, k, v, AttentionConfig(16, 8, 128, True, 62), FLASH_DECODE, 32, 128)
+    assert p["splits"] == 2
+    p = plan(q, k, v, AttentionConfig(16, 8, 128, False, 62), FLASH_DECODE, 32, 128)
+    assert p["splits"] == 3
+
+
+def test_kernel_choice_and_layout_fallback():
+    q, k, v, cfg = _decode()
+    assert plan(q, k, v, cfg, REFERENCE)["kernel"] == "attn_naive"
+    assert plan(q, k, v, cfg, DECODE_SPLIT_KV)["kernel"] == "attn_rows"
+    # head-major cache view [L, Hkv, D] with strides (D, cap * D, 1)
+    kh = tensor((2048, 8, 128), strides=(128, 4096 * 128, 1))
+    assert plan(q, kh, kh, cfg, FLASH_DECODE)["kernel"] == "attn_rows"
+    # rows that are not 16-byte aligned cannot feed 128-bit loads
+    odd = tensor((2048, 8, 128), strides=(1028, 128, 1))
+    assert plan(q, odd, odd, cfg, FLASH_DECODE)["kernel"] == "attn_naive"
+
+
+def test_split_k_sizes_cover_the_window():
+    for L in (1, 63, 64, 65, 256, 640, 2048, 8192, 20480):
+        q, k, v, cfg = _decode(L=L)
+        p = plan(q, k, v, cfg, DECODE_SPLIT_KV)
+        assert p["splits"] * p["block_keys"] >= L
+        assert (p["splits"] - 1) * p["block_keys"] < L
+        if p["splits"] > 1:
+            assert p["scratch_bytes"] == 8 * p["splits"] * 2 * 130 * 4
+
+
+# ---------------------------------------- policy (qwen3.rs:799-822) -------
+
+def test_kind_policy_matches_reference_cases():
+    kind = mi_attn.attention_kind_for_tokens
+    # qwen3.rs:1044-1081
+    assert kind(TILED, 1, 640, 2) == FLASH_DECODE
+    assert kind(TILED, 1, 255, 2) == DECODE_SPLIT_KV
+    assert kind(TILED, 31, 31, 2) == TILED
+    assert kind(TILED, 32, 32, 2) == FLASH_PREFILL
+    assert kind(TILED, 512, 512, 2) == FLASH_PREFILL
+    assert kind(REFERENCE, 1, 640, 2) == REFERENCE
+    # generalised: the split-K kernel serves ratio 4 too (reference: DecodeSplitKv)
+    assert kind(TILED, 1, 640, 4) == FLASH_DECODE
+    assert kind(FLASH_DECODE, 8, 640, 2) == TILED
+    assert kind(DECODE_SPLIT_KV, 1, 640, 2) == DECODE_SPLIT_KV
+    assert kind(FLASH_PREFILL, 1, 300, 8) == FLASH_DECODE
+    assert kind(FLASH_PREFILL, 1, 100, 8) == DECODE_SPLIT_KV
+
+
+# ---------------------------------------------- tensor views ---------------
+
+def test_prefix_and_reshape():
+    t = tensor((4096, 8, 128), strides=(128, 4096 * 128, 1))
+    p = t.prefix(2048)
+    assert p.shape == (2048, 8, 128) and p.strides == t.strides and p.data_ptr == t.data_ptr
+    with pytest.raises(MiError, match="outside capacity"):
+        t.prefix(0)
+    with pytest.raises(MiError, match="outside capacity"):
+        t.prefix(4097)
+    c = tensor((4, 6))
+    assert c.reshape((2, 12)).shape == (2, 12)
+    with pytest.raises(MiError):
+        c.reshape((5, 5))
+    with pytest.raises(MiError, match="contiguous"):
+        t.reshape((4096, 1024))

@@ -1,0 +1,186 @@
+"""GPU parity of the attention kernels, through the C ABI, against the oracle.
+
+The bar (north_star): max-abs error <= 2e-3 against the f32 oracle
+(attention_reference_f16 restated, unrounded) on identical inputs; the
+golden fixtures (torch float64 SDPA) are checked with the same bound. The
+reference tests' own tolerance was 0.02 (gpu.rs:6).
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import mi_attn
+import ref_cases
+import workloads
+from helpers import (KINDS, TOL, assert_parity, f16, max_abs, oracle_attention, run_attention,
+                     upload_kv)
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_golden.npz"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    data = np.load(GOLDEN, allow_pickle=False)
+    return {name: data[name] for name in data["__names__"].tolist()}
+
+
+CASES = ref_cases.attention_cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c["name"])
+def test_reference_cases_all_kinds(ctx, case, golden):
+    """gpu.rs:613-808 / ops.rs:1416-1476 shapes and inputs, every kind."""
+    q, k, v = ref_cases.build(case)
+    geo = dict(hq=case["hq"], hkv=case["hkv"], d=case["d"], off=case["off"])
+    ref = oracle_attention(q, k, v, **geo)
+    for kind in case["kinds"]:
+        for layout in ("head_major", "position_major"):
+            out = run_attention(ctx, q, k, v, kind=kind, layout=layout, **geo)
+            label = f"{case['name']}/{kind}/{layout}"
+            assert_parity(out, ref, label=label)
+            assert max_abs(out, golden[case["name"]]) <= TOL, label
+
+
+@pytest.mark.parametrize("L", [1, 63, 64, 65, 256, 640, 8192])
+def test_flash_decode_block_and_thread_grid(ctx, L):
+    """gpu.rs:729-768: every (block, threads) configuration."""
+    case = next(c for c in CASES if c["name"] == f"decode_blocks_L{L}")
+    q, k, v = ref_cases.build(case)
+    geo = dict(hq=2, hkv=1, d=128, off=L - 1)
+    ref = oracle_attention(q, k, v, **geo)
+    for block in (32, 64, 128, 256):
+        for threads in (128, 256):
+            out = run_attention(ctx, q, k, v, kind="flash-decode", block=block, threads=threads,
+                                **geo)
+            assert_parity(out, ref, label=f"L={L} block={block} threads={threads}")
+
+
+def test_reference_kind_is_the_exact_two_pass_softmax(ctx):
+    """The GPU Reference kernel follows the oracle's operation order: only
+    expf may differ (by an ulp), so outputs agree to within one f16 ulp."""
+    rng = np.random.default_rng(5)
+    T, L, hq, hkv, d = 17, 40, 8, 2, 64
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=L - T)
+    ref = oracle_attention(q, k, v, **geo)
+    out = run_attention(ctx, q, k, v, kind="reference", **geo)
+    ulps = np.abs(out.astype(np.int32) - ref["f16"].astype(np.int32))
+    assert ulps.max() <= 1
+    assert (ulps != 0).mean() < 0.01
+    assert_parity(out, ref)
+
+
+# -------------------------------------------------- BASELINE configs ------
+
+def _prefill_parity(ctx, c, kind, rows=None):
+    geo = dict(hq=c.q_heads, hkv=c.kv_heads, d=c.head_dim, off=c.query_offset)
+    out = run_attention(ctx, c.q, c.k, c.v, kind=kind, **geo)
+    ref = oracle_attention(c.q, c.k, c.v, rows=rows, **geo)
+    got = out if rows is None else out[rows]
+    return assert_parity(got, ref, label=f"c{c.config}/{kind}")
+
+
+def test_c1_prefill_seeded(ctx):
+    c = workloads.case(1)
+    for kind in ("flash-prefill", "tiled", "reference"):
+        _prefill_parity(ctx, c, kind)
+
+
+def test_c2_decode_seeded(ctx):
+    c = workloads.case(2)
+    for kind in ("flash-decode", "decode-split-kv", "reference"):
+        _prefill_parity(ctx, c, kind)
+
+
+def test_c3_prefill_seeded(ctx):
+    c = workloads.case(3)
+    _prefill_parity(ctx, c, "flash-prefill")
+
+
+def test_c4_batched_decode_seeded(ctx):
+    """B=32 sequences, lengths ~ U[1024, 8192], one launch over all of them."""
+    c = workloads.case(4)
+    B, hq, hkv, d, cap = c.batch, c.q_heads, c.kv_heads, c.head_dim, c.kv_length
+    kstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
+    vstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
+    for b in range(B):
+        kstore[b, :, : c.lengths[b]] = c.k[b].transpose(1, 0, 2)
+        vstore[b, :, : c.lengths[b]] = c.v[b].transpose(1, 0, 2)
+    kt, vt = ctx.tensor(kstore), ctx.tensor(vstore)
+    view = ((B, cap, hkv, d), (hkv * cap * d, d, cap * d, 1))
+    kview, vview = kt.view(*view), vt.view(*view)
+    qt = ctx.tensor(c.q)
+    lengths = ctx.tensor(c.lengths, mi_attn.U32)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    for block in (0, 256, 1024):
+        batch = ctx.begin_batch()
+        out = batch.attention_decode_batched(qt, kview, vview, lengths, cfg, block)
+        batch.finish()
+        got = ctx.download(out)
+        worst = 0.0
+        for b in range(B):
+            ref = oracle_attention(c.q[b:b + 1], c.k[b], c.v[b], hq=hq, hkv=hkv, d=d,
+                                   off=int(c.lengths[b]) - 1)
+            worst = max(worst, assert_parity(got[b:b + 1], ref, label=f"seq {b} block {block}"))
+        print(f"c4 block={block}: max-abs {worst:.2e}")
+
+
+# --------------------------------------------------------- invariants -----
+
+def test_masked_keys_do_not_influence_output(ctx):
+    rng = np.random.default_rng(7)
+    T, L, hq, hkv, d, off = 3, 300, 16, 8, 128, 200
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+    k2, v2 = k.copy(), v.copy()
+    k2[off + T:] = np.float16(30.0).view(np.uint16)
+    v2[off + T:] = np.float16(-9.0).view(np.uint16)
+    for kind in ("tiled", "flash-prefill", "reference"):
+        a = run_attention(ctx, q, k, v, kind=kind, **geo)
+        b = run_attention(ctx, q, k2, v2, kind=kind, **geo)
+        assert (a == b).all(), kind
+    a = run_attention(ctx, q[:1], k, v, kind="flash-decode", **geo)
+    b = run_attention(ctx, q[:1], k2, v2, kind="flash-decode", **geo)
+    assert (a == b).all()
+
+
+def test_layouts_give_identical_bits(ctx):
+    c = workloads.case(2)
+    geo = dict(hq=c.q_heads, hkv=c.kv_heads, d=c.head_dim, off=c.query_offset)
+    a = run_attention(ctx, c.q, c.k, c.v, kind="flash-decode", layout="head_major", **geo)
+    b = run_attention(ctx, c.q, c.k, c.v, kind="flash-decode", layout="position_major", **geo)
+    assert (a == b).all()
+
+
+def test_decode_matches_last_prefill_row_and_chunked_prefill(ctx):
+    rng = np.random.default_rng(9)
+    T, hq, hkv, d = 96, 16, 8, 128
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((T, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((T, hkv, d)).astype(np.float16).view(np.uint16)
+    full = run_attention(ctx, q, k, v, kind="flash-prefill", hq=hq, hkv=hkv, d=d, off=0)
+    dec = run_attention(ctx, q[-1:], k, v, kind="flash-decode", hq=hq, hkv=hkv, d=d, off=T - 1)
+    assert max_abs(dec, f16(full[-1:])) <= 2 * TOL
+    P = 40
+    chunk = run_attention(ctx, q[P:], k, v, kind="flash-prefill", hq=hq, hkv=hkv, d=d, off=P)
+    assert max_abs(chunk, f16(full[P:])) <= 2 * TOL
+
+
+def test_gqa_equals_mha_with_repeated_heads(ctx):
+    rng = np.random.default_rng(11)
+    T, L, hq, hkv, d = 4, 500, 32, 8, 128
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    gqa = run_attention(ctx, q, k, v, kind="tiled", hq=hq, hkv=hkv, d=d, off=L - T)
+    mha = run_attention(ctx, q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), kind="tiled",
+                        hq=hq, hkv=hq, d=d, off=L - T)
+    assert max_abs(gqa, f16(mha)) <= 2 * TOL

@@ -1,0 +1,154 @@
+"""GPU tests of the head-major KV cache: append, fused Q/K norm + RoPE with
+K-append, cache bookkeeping, and a decode loop in forward_layer's order
+(crates/metal-infer-models/src/qwen3.rs:704-750)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mi_attn
+import oracle
+from helpers import TOL, assert_parity, f16, oracle_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def rand(seed, shape, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(
+        np.float16).view(np.uint16)
+
+
+def test_copy_into_cache_is_bit_exact_head_major(ctx):
+    hkv, d, cap = 8, 128, 64
+    cache = ctx.kv_cache(1, hkv, d, cap)
+    key, value = cache.layer(0)
+    assert key.shape == (cap, hkv, d) and key.strides == (d, cap * d, 1)
+    sentinel = np.full((cap, hkv, d), 0x7bff, dtype=np.uint16)
+    ctx.upload(key, sentinel)
+    src = rand(1, (5, hkv, d))
+    ctx.copy_into_cache(ctx.tensor(src), key, 17)
+    got = ctx.download(key)
+    expected = sentinel.copy()
+    expected[17:22] = src
+    assert (got == expected).all()
+    # the storage really is head-major: [Hkv, cap, D]
+    raw = ctx.download(key.view((hkv, cap, d), (cap * d, d, 1)))
+    assert (raw[:, 17:22] == src.transpose(1, 0, 2)).all()
+    cache.close()
+
+
+def test_copy_into_cache_errors(ctx):
+    cache = ctx.kv_cache(1, 2, 16, 8)
+    key, _ = cache.layer(0)
+    batch = ctx.begin_batch()
+    with pytest.raises(mi_attn.MiError, match="KV cache capacity exceeded"):
+        batch.copy_into_cache(ctx.tensor(rand(2, (3, 2, 16))), key, 6)
+    with pytest.raises(mi_attn.MiError, match="incompatible"):
+        batch.copy_into_cache(ctx.tensor(rand(2, (3, 4, 16))), key, 0)
+    with pytest.raises(mi_attn.MiError) as err:
+        batch.copy_into_cache(ctx.tensor(np.zeros((3, 2, 16), np.float32), mi_attn.F32), key, 0)
+    assert err.value.name == "MI_ERR_DTYPE"
+    batch.abandon()
+    cache.close()
+
+
+def test_kv_cache_bookkeeping(ctx):
+    with pytest.raises(mi_attn.MiError, match="capacity must be non-zero"):
+        ctx.kv_cache(2, 8, 128, 0)
+    cache = ctx.kv_cache(28, 8, 128, 2048)
+    assert len(cache) == 0 and cache.capacity == 2048
+    cache.set_len(513)
+    assert len(cache) == 513
+    with pytest.raises(mi_attn.MiError) as err:
+        cache.set_len(2049)
+    assert err.value.name == "MI_ERR_CACHE_CAPACITY"
+    cache.reset()
+    assert len(cache) == 0
+    k0, v0 = cache.layer(0)
+    k27, _ = cache.layer(27)
+    assert v0.data_ptr - k0.data_ptr == 8 * 2048 * 128 * 2
+    assert k27.data_ptr - k0.data_ptr == 27 * 2 * 8 * 2048 * 128 * 2
+    with pytest.raises(mi_attn.MiError, match="missing KV cache layer"):
+        cache.layer(28)
+    cache.close()
+
+
+def _qk_case(ctx, q, k, qw, kw, offset, theta, eps, cap):
+    T, hkv, d = k.shape
+    cache = ctx.kv_cache(1, hkv, d, cap)
+    key, _ = cache.layer(0)
+    ctx.upload(key, np.zeros((cap, hkv, d), dtype=np.uint16))
+    batch = ctx.begin_batch()
+    q_out = batch.qk_norm_rope_cache(ctx.tensor(q), ctx.tensor(k), ctx.tensor(qw), ctx.tensor(kw),
+                                     key, mi_attn.QkNormRopeCacheConfig(offset, theta, eps))
+    batch.finish()
+    got_q, got_cache = ctx.download(q_out), ctx.download(key)
+    cache.close()
+    return got_q, got_cache
+
+
+def test_qk_norm_rope_cache_reference_case(ctx):
+    """gpu.rs:540-576: Q = i/16 - 1, K = i/12 - 0.5, weights 0.75 + i/16,
+    offset 1; K lands in cache rows 1..2 and nowhere else."""
+    f = np.float32
+    q = (np.arange(32, dtype=f) / f(16) - f(1)).astype(np.float16).view(np.uint16).reshape(2, 2, 8)
+    k = (np.arange(16, dtype=f) / f(12) - f(0.5)).astype(np.float16).view(np.uint16).reshape(2, 1, 8)
+    w = (f(0.75) + np.arange(8, dtype=f) / f(16)).astype(np.float16).view(np.uint16)
+    got_q, got_cache = _qk_case(ctx, q, k, w, w, 1, 10_000.0, 1e-6, 4)
+    want_q, want_k = oracle.qk_norm_rope(q, k, w, w, offset=1, theta=10_000.0, epsilon=1e-6)
+    assert np.abs(got_q.astype(np.int32) - want_q.astype(np.int32)).max() <= 1
+    assert np.abs(got_cache[1:3].astype(np.int32) - want_k.astype(np.int32)).max() <= 1
+    assert (got_cache[0] == 0).all() and (got_cache[3] == 0).all()
+
+
+@pytest.mark.parametrize("offset", [0, 300, 16384])
+def test_qk_norm_rope_cache_seeded(ctx, offset):
+    T, hq, hkv, d, theta, eps = 7, 16, 8, 128, 1_000_000.0, 1e-6
+    q, k = rand(3, (T, hq, d)), rand(4, (T, hkv, d))
+    qw = (1 + 0.1 * np.random.default_rng(5).standard_normal(d)).astype(np.float16).view(np.uint16)
+    kw = (1 + 0.1 * np.random.default_rng(6).standard_normal(d)).astype(np.float16).view(np.uint16)
+    got_q, got_cache = _qk_case(ctx, q, k, qw, kw, offset, theta, eps, offset + T)
+    want_q, want_k = oracle.qk_norm_rope(q, k, qw, kw, offset=offset, theta=theta, epsilon=eps)
+    # f32 sin/cos of the same f32 angle: at most one f16 ulp apart, except
+    # where the rotation cancels (checked against the pair magnitude).
+    for got, want in ((got_q, want_q), (got_cache[offset:], want_k)):
+        diff = np.abs(f16(got).astype(np.float64) - f16(want))
+        mag = np.abs(f16(want)).max()
+        assert diff.max() <= max(2e-3, 2e-3 * mag), (offset, diff.max())
+
+
+def test_decode_loop_in_forward_layer_order(ctx):
+    """Per step: Q/K norm+RoPE with K into the cache, V appended, then
+    attention over the cache prefix (qwen3.rs:704-750), all in one batch."""
+    hq, hkv, d, cap, prompt, steps = 16, 8, 128, 512, 300, 4
+    theta, eps = 1_000_000.0, 1e-6
+    qw = np.full(d, np.float16(1.0).view(np.uint16), dtype=np.uint16)
+    cache = ctx.kv_cache(1, hkv, d, cap)
+    key, value = cache.layer(0)
+    k_rows, v_rows = [], []
+    qwt, kwt = ctx.tensor(qw), ctx.tensor(qw)
+    for step in range(steps):
+        T = prompt if step == 0 else 1
+        offset = len(cache)
+        q, k, v = rand(10 + step, (T, hq, d)), rand(20 + step, (T, hkv, d)), rand(30 + step, (T, hkv, d))
+        batch = ctx.begin_batch()
+        q_rot = batch.qk_norm_rope_cache(ctx.tensor(q), ctx.tensor(k), qwt, kwt, key,
+                                         mi_attn.QkNormRopeCacheConfig(offset, theta, eps))
+        batch.copy_into_cache(ctx.tensor(v), value, offset)
+        active = offset + T
+        kind = mi_attn.attention_kind_for_tokens(mi_attn.TILED, T, active, hq // hkv)
+        cfg = mi_attn.AttentionConfig(hq, hkv, d, True, offset)
+        out = batch.attention(q_rot, key.prefix(active), value.prefix(active), cfg, kind)
+        batch.finish()
+        cache.set_len(active)
+        want_q, want_k = oracle.qk_norm_rope(q, k, qw, qw, offset=offset, theta=theta, epsilon=eps)
+        k_rows.append(want_k)
+        v_rows.append(v)
+        got_q = ctx.download(q_rot)
+        kk, vv = np.concatenate(k_rows), np.concatenate(v_rows)
+        ref = oracle_attention(got_q, ctx.download(key.prefix(active)), vv, hq=hq, hkv=hkv, d=d,
+                               off=offset)
+        assert_parity(ctx.download(out), ref, label=f"step {step} kind {kind}")
+        assert np.abs(ctx.download(key.prefix(active)).astype(np.int32)
+                      - kk.astype(np.int32)).max() <= 1
+    cache.close()

@@ -1,0 +1,108 @@
+"""GPU tests of the runtime: batches, scratch leases, profiling, errors
+(context.rs behaviour; gpu.rs:578-611)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mi_attn
+from helpers import run_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def rand(seed, shape):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float16).view(np.uint16)
+
+
+def _decode_inputs(ctx, L=1024, hq=16, hkv=8, d=128):
+    q, k, v = rand(1, (1, hq, d)), rand(2, (L, hkv, d)), rand(3, (L, hkv, d))
+    return (ctx.tensor(q), ctx.tensor(k), ctx.tensor(v),
+            mi_attn.AttentionConfig(hq, hkv, d, True, L - 1))
+
+
+def test_batched_dependent_work_matches_eager(ctx):
+    """gpu.rs:578-597: dependent work in one batch == one batch per op."""
+    q, k, v, cfg = _decode_inputs(ctx)
+    eager = ctx.download(ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE))
+    batch = ctx.begin_batch()
+    first = batch.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+    # second op reads the first op's output as its query
+    second = batch.attention(first, k, v, cfg, mi_attn.DECODE_SPLIT_KV)
+    batch.finish()
+    assert (ctx.download(first) == eager).all()
+    again = ctx.download(ctx.attention(ctx.tensor(eager), k, v, cfg, mi_attn.DECODE_SPLIT_KV))
+    assert (ctx.download(second) == again).all()
+
+
+def test_invalid_batch_can_be_abandoned(ctx):
+    """gpu.rs:599-611."""
+    q, k, v, cfg = _decode_inputs(ctx)
+    batch = ctx.begin_batch()
+    with pytest.raises(mi_attn.MiError):
+        batch.attention(q, k, v, mi_attn.AttentionConfig(16, 4, 128, True, 0), mi_attn.TILED)
+    batch.abandon()
+    out = ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+    assert ctx.download(out).shape == (1, 16, 128)
+
+
+def test_commit_wait_and_stats(ctx):
+    q, k, v, cfg = _decode_inputs(ctx)
+    batch = ctx.begin_batch()
+    batch.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+    batch.commit()
+    stats = batch.wait()
+    assert stats.gpu_ns > 0 and stats.wall_ns > 0
+
+
+def test_kernel_profiling_records_each_launch(ctx):
+    q, k, v, cfg = _decode_inputs(ctx)
+    ctx.take_kernel_profiles()
+    ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+    assert ctx.take_kernel_profiles() == []
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        batch.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+        batch.attention(q, k, v, cfg, mi_attn.REFERENCE)
+        batch.finish()
+        profiles = ctx.take_kernel_profiles()
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert [name for name, _ in profiles] == ["attn_rows", "attn_naive"]
+    assert all(ns > 0 for _, ns in profiles)
+
+
+def test_scratch_leases_are_reused_after_release(ctx):
+    batch = ctx.begin_batch()
+    a = batch.empty((1024, 16))
+    ptr = a.data_ptr
+    assert ptr % 256 == 0
+    b = batch.empty((8,))
+    assert b.data_ptr != ptr
+    a.free()
+    c = batch.empty((512, 16))
+    assert c.data_ptr == ptr
+    batch.finish()
+    # a lease outlives its batch and stays readable
+    ctx.upload(c, np.arange(512 * 16, dtype=np.uint16).reshape(512, 16))
+    assert (ctx.download(c).reshape(-1) == np.arange(512 * 16)).all()
+
+
+def test_allocated_bytes_tracks_tensors(ctx):
+    before = ctx.allocated_bytes()
+    t = ctx.empty((1 << 20,))
+    assert ctx.allocated_bytes() == before + (1 << 21)
+    t.free()
+    assert ctx.allocated_bytes() == before
+
+
+def test_tuned_flash_decode_table_is_used(ctx):
+    ctx.tune_flash_decode(16, 8, 128)
+    for length in (512, 2048, 8192):
+        block, threads = ctx.flash_decode_configuration_for_length(length)
+        assert block in (32, 64, 128, 256) and threads in (128, 256)
+    rng_q = rand(7, (1, 16, 128))
+    k, v = rand(8, (700, 8, 128)), rand(9, (700, 8, 128))
+    out = run_attention(ctx, rng_q, k, v, kind="flash-decode", hq=16, hkv=8, d=128, off=699)
+    assert out.shape == (1, 16, 128)
