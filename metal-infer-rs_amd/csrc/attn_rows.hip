@@ -12,10 +12,11 @@
 //    128-bit load, so a wave reads 64 * 16 B contiguous bytes per load;
 //  - per-row dot products reduce with DPP inside a 16-lane row;
 //  - scores and the softmax stay in f32 (v_exp_f32 on log2-scaled scores);
-//  - the split-K merge is fused: the last workgroup of a (row, KV head) to
-//    finish merges every split's (max, sum, acc[D]) partial, so a decode is
-//    one launch. Arrival counters are reset by that workgroup, so they are
-//    zero between launches without any memset.
+//  - with more than one split, each split writes a (max, sum, acc[D])
+//    partial and attn_merge_kernel combines them. Publishing partials inside
+//    one kernel needs an agent-scope release per workgroup, which on a
+//    multi-XCD part writes back the XCD's whole L2; measured slower than the
+//    second launch for every split size, so the kernel boundary does it.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -72,6 +73,69 @@ __device__ __forceinline__ float dot(const Vec<VEC> &a, const Vec<VEC> &b) {
   }
 }
 
+// Log-sum-exp combine of a unit's split partials, the reference's reduce
+// kernels (transformer.metal:2251-2316). Partials are staged through LDS a
+// chunk at a time with every load in flight, then folded with an online
+// rescale, so the cost is one memory round trip per chunk.
+constexpr int kMergeFloats = 6144;
+
+template <int D, int GC, int THREADS>
+__device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
+                                             uint32_t nsplits, uint16_t *out,
+                                             float *buf) {
+  constexpr int ROW = D + 2;  // (max, sum, acc[D]) per split and head
+  constexpr int SPLITS =
+      (kMergeFloats / (GC * ROW)) > 0 ? kMergeFloats / (GC * ROW) : 1;
+  constexpr int ITEMS = (GC * D + THREADS - 1) / THREADS;
+  const int tid = threadIdx.x;
+  const float *base = p.partial + (size_t)unit * p.max_splits * GC * ROW;
+  float M[ITEMS], L[ITEMS], A[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) M[i] = -INFINITY, L[i] = 0.0f, A[i] = 0.0f;
+  for (uint32_t s0 = 0; s0 < nsplits; s0 += SPLITS) {
+    const uint32_t n = min((uint32_t)SPLITS, nsplits - s0);
+    const float *src = base + (size_t)s0 * GC * ROW;
+    const uint32_t total = n * GC * ROW;
+    // All of a thread's loads are issued before its first LDS write.
+    float staged[kMergeFloats / THREADS + 1];
+#pragma unroll
+    for (int j = 0; j < kMergeFloats / THREADS + 1; ++j) {
+      const uint32_t i = tid + j * THREADS;
+      staged[j] = i < total ? src[i] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kMergeFloats / THREADS + 1; ++j) {
+      const uint32_t i = tid + j * THREADS;
+      if (i < total) buf[i] = staged[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = tid + i * THREADS;
+      if (idx >= GC * D) break;
+      const int g = idx / D, d = idx % D;
+      float cm = M[i];
+      for (uint32_t s = 0; s < n; ++s) cm = fmaxf(cm, buf[(s * GC + g) * ROW]);
+      const float rescale = M[i] == -INFINITY ? 0.0f : exp2_raw(M[i] - cm);
+      float l = L[i] * rescale, a = A[i] * rescale;
+      for (uint32_t s = 0; s < n; ++s) {
+        const float *ps = buf + (s * GC + g) * ROW;
+        const float f = exp2_raw(ps[0] - cm);
+        l += ps[1] * f;
+        a += ps[2 + d] * f;
+      }
+      M[i] = cm, L[i] = l, A[i] = a;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = tid + i * THREADS;
+    if (idx >= GC * D) break;
+    out[(idx / D) * p.o_head + idx % D] = f32_to_f16(A[i] / L[i]);
+  }
+}
+
 template <int D, int WAVES, int GC>
 __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     const RowsParams p) {
@@ -85,7 +149,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   __shared__ float s_m[WAVES][GC];
   __shared__ float s_l[WAVES][GC];
   __shared__ float s_acc[WAVES][GC][D];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -149,22 +212,32 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     for (int i = 0; i < VEC; ++i) acc[g][i] = 0.0f;
   }
 
+  // Loads are unconditional: past the split's end a lane re-reads the last
+  // key row (always in bounds) and its score is masked to -inf, so every
+  // batch of 2*U loads issues back to back. The next batch is in flight
+  // while the current one is consumed.
+  auto load_batch = [&](uint32_t first, Vec<VEC> *kd, Vec<VEC> *vd) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t kk = min(first + (uint32_t)(u * R), k1 - 1);
+      kd[u] = load_vec<VEC>(kb + (int64_t)kk * p.k_pos);
+      vd[u] = load_vec<VEC>(vb + (int64_t)kk * p.v_pos);
+    }
+  };
+  Vec<VEC> kv[U], vv[U];
+  uint32_t key = k0 + row;
+  if (key < k1) load_batch(key, kv, vv);
   // Every lane of a key row shares `row`, so the DPP reductions below only
   // ever combine lanes with identical trip counts.
-  for (uint32_t key = k0 + row; key < k1; key += R * U) {
-    Vec<VEC> kv[U], vv[U];
+  for (; key < k1; key += R * U) {
+    const uint32_t next = key + R * U;
+    Vec<VEC> kn[U], vn[U];
+    if (next < k1) load_batch(next, kn, vn);
     bool valid[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t kk = key + u * R;
-      valid[u] = kk < k1;
-      if (valid[u]) {
-        kv[u] = load_vec<VEC>(kb + (int64_t)kk * p.k_pos);
-        vv[u] = load_vec<VEC>(vb + (int64_t)kk * p.v_pos);
-      } else {
-        kv[u] = zero_vec<VEC>();
-        vv[u] = zero_vec<VEC>();
-      }
+      valid[u] = key + (uint32_t)(u * R) < k1;
+      if (!valid[u]) vv[u] = zero_vec<VEC>();
     }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
@@ -194,6 +267,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         acc[g][i] = a;
       }
       m[g] = mx;
+    }
+    if (next < k1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) kv[u] = kn[u], vv[u] = vn[u];
     }
   }
 
@@ -257,59 +334,59 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
       }
     }
   }
-  if (direct) return;
+}
 
-  // Publish the partial, count arrivals; the last split merges.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[unit], 1u);
-    s_last = prev == nsplits - 1;
+// Merges the split partials of one (row, KV head, head chunk) unit: the
+// log-sum-exp combine of the reference's reduce kernels
+// (transformer.metal:2251-2316). Launched after attn_rows_kernel on the same
+// stream, so every partial is visible without any in-kernel fence.
+template <int D, int GC>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const RowsParams p) {
+  __shared__ float buf[kMergeFloats];
+  const uint32_t unit = blockIdx.x;
+  const uint32_t units_per_token = p.kv_heads * p.head_chunks;
+  const uint32_t bt = unit / units_per_token;
+  const uint32_t rest = unit % units_per_token;
+  const uint32_t kvh = rest / p.head_chunks, hc = rest % p.head_chunks;
+  const uint32_t b = bt / p.tokens, t = bt % p.tokens;
+  uint32_t len = p.kv_length, off = p.query_offset;
+  if (p.lengths != nullptr) {
+    len = min(p.lengths[b], p.kv_length);
+    off = len >= p.tokens ? len - p.tokens : 0u;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float *base = p.partial + (size_t)unit * p.max_splits * GC * (D + 2);
-  for (int idx = tid; idx < GC * D; idx += THREADS) {
-    const int g = idx / D, d = idx % D;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < nsplits; ++s)
-      M = fmaxf(M, base[(s * GC + g) * (D + 2)]);
-    float L = 0.0f, A = 0.0f;
-    for (uint32_t s = 0; s < nsplits; ++s) {
-      const float *ps = base + (s * GC + g) * (D + 2);
-      const float f = exp2_raw(ps[0] - M);
-      L += ps[1] * f;
-      A += ps[2 + d] * f;
-    }
-    out[g * p.o_head + d] = f32_to_f16(A / L);
-  }
-  if (tid == 0) atomicExch(&p.counters[unit], 0u);
+  const uint64_t window = (uint64_t)off + t + 1;
+  const uint32_t available =
+      p.causal != 0 ? (uint32_t)min((uint64_t)len, window) : len;
+  const uint32_t nsplits = (available + p.block_keys - 1) / p.block_keys;
+  if (nsplits <= 1) return;  // written directly by the split kernel
+  const uint32_t h0 = kvh * p.group + hc * GC;
+  uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)t * p.o_tok +
+                  (int64_t)h0 * p.o_head;
+  merge_splits<D, GC, 256>(p, unit, nsplits, out, buf);
+}
+
+template <int D, int WAVES, int GC>
+hipError_t launch_rows_dwg(const RowsParams &p, hipStream_t stream) {
+  const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
+                  p.batch * p.tokens);
+  attn_rows_kernel<D, WAVES, GC><<<grid, WAVES * 64, 0, stream>>>(p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || p.max_splits <= 1) return err;
+  const uint32_t units = p.batch * p.tokens * p.kv_heads * p.head_chunks;
+  attn_merge_kernel<D, GC><<<units, 256, 0, stream>>>(p);
+  return hipGetLastError();
 }
 
 template <int D, int WAVES>
 hipError_t launch_rows_dw(const RowsParams &p, uint32_t chunk,
                           hipStream_t stream) {
-  const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
-                  p.batch * p.tokens);
-  const dim3 block(WAVES * 64);
   switch (chunk) {
-    case 8:
-      attn_rows_kernel<D, WAVES, 8><<<grid, block, 0, stream>>>(p);
-      break;
-    case 4:
-      attn_rows_kernel<D, WAVES, 4><<<grid, block, 0, stream>>>(p);
-      break;
-    case 2:
-      attn_rows_kernel<D, WAVES, 2><<<grid, block, 0, stream>>>(p);
-      break;
-    case 1:
-      attn_rows_kernel<D, WAVES, 1><<<grid, block, 0, stream>>>(p);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case 8: return launch_rows_dwg<D, WAVES, 8>(p, stream);
+    case 4: return launch_rows_dwg<D, WAVES, 4>(p, stream);
+    case 2: return launch_rows_dwg<D, WAVES, 2>(p, stream);
+    case 1: return launch_rows_dwg<D, WAVES, 1>(p, stream);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 template <int D>

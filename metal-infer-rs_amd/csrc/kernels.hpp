@@ -22,7 +22,6 @@ struct RowsParams {
   uint16_t *out;
   int64_t o_seq, o_tok, o_head;
   float *partial;           // [units][max_splits][chunk][D + 2] f32
-  uint32_t *counters;       // [units] arrival counters, zero between calls
   const uint32_t *lengths;  // per-sequence KV length, or null
   uint32_t batch;           // B
   uint32_t tokens;          // T

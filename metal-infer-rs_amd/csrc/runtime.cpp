@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 namespace mi {
@@ -184,29 +185,7 @@ mi_status scratch_free(Context *ctx, void *ptr) {
   return MI_OK;
 }
 
-mi_status ensure_counters(Context *ctx, size_t count) {
-  if (count <= ctx->counter_capacity) return MI_OK;
-  size_t capacity = std::max<size_t>(count, 4096);
-  capacity = align_up(capacity, 4096);
-  hipError_t err = hipStreamSynchronize(ctx->stream);
-  if (err != hipSuccess) return hip_fail(MI_ERR_COMMAND, "stream", err);
-  if (ctx->counters != nullptr) {
-    hipFree(ctx->counters);
-    ctx->allocated -= ctx->counter_capacity * sizeof(uint32_t);
-    ctx->counters = nullptr;
-    ctx->counter_capacity = 0;
-  }
-  err = hipMalloc(&ctx->counters, capacity * sizeof(uint32_t));
-  if (err != hipSuccess) return hip_fail(MI_ERR_RESOURCE, "split-K counters", err);
-  err = hipMemset(ctx->counters, 0, capacity * sizeof(uint32_t));
-  if (err != hipSuccess) return hip_fail(MI_ERR_RESOURCE, "split-K counters", err);
-  ctx->counter_capacity = capacity;
-  ctx->allocated += capacity * sizeof(uint32_t);
-  return MI_OK;
-}
-
 }  // namespace mi
-
 
 using namespace mi;
 
@@ -255,11 +234,6 @@ mi_status mi_context_create(int32_t device, mi_context **out) {
   // Default priority only: streams of other priorities are not used.
   err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (err != hipSuccess) return hip_fail(MI_ERR_RESOURCE, "command stream", err);
-  mi_status st = ensure_counters(ctx.get(), 1 << 16);
-  if (st != MI_OK) {
-    hipStreamDestroy(ctx->stream);
-    return st;
-  }
   *out = ctx.release();
   return MI_OK;
 }
@@ -271,7 +245,11 @@ void mi_context_destroy(mi_context *ctx) {
   for (auto &pool : ctx->pools)
     for (auto &chunk : pool->chunks) hipFree(chunk.base);
   for (auto &entry : ctx->tensors) hipFree(reinterpret_cast<void *>(entry.first));
-  if (ctx->counters) hipFree(ctx->counters);
+  for (mi_kv_cache *cache : ctx->caches) {
+    hipFree(cache->base);
+    cache->base = nullptr;
+    cache->ctx = nullptr;
+  }
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -575,17 +553,22 @@ mi_status mi_kv_cache_create(mi_context *ctx, uint32_t layers, uint32_t kv_heads
   cache->kv_heads = kv_heads;
   cache->head_dim = head_dim;
   cache->capacity = capacity;
+  ctx->caches.insert(cache);
   *out = cache;
   return MI_OK;
 }
 
 void mi_kv_cache_destroy(mi_kv_cache *cache) {
   if (cache == nullptr) return;
-  hipSetDevice(cache->ctx->device);
-  hipStreamSynchronize(cache->ctx->stream);
-  hipFree(cache->base);
-  cache->ctx->allocated -= (uint64_t)cache->kv_heads * cache->capacity *
-                           cache->head_dim * 2 * cache->layers * sizeof(uint16_t);
+  Context *ctx = cache->ctx;
+  if (ctx != nullptr) {  // else its context already released the storage
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    hipFree(cache->base);
+    ctx->allocated -= (uint64_t)cache->kv_heads * cache->capacity * cache->head_dim * 2 *
+                      cache->layers * sizeof(uint16_t);
+    ctx->caches.erase(cache);
+  }
   delete cache;
 }
 
@@ -610,6 +593,7 @@ mi_status mi_kv_cache_layer(const mi_kv_cache *cache, uint32_t layer,
   if (cache == nullptr || key == nullptr || value == nullptr)
     return fail(MI_ERR_INVALID_ARGUMENT, "null cache or output");
   if (layer >= cache->layers) return fail(MI_ERR_SHAPE, "missing KV cache layer");
+  if (cache->ctx == nullptr) return fail(MI_ERR_RESOURCE, "KV cache outlived its context");
   const uint64_t per_tensor = (uint64_t)cache->kv_heads * cache->capacity * cache->head_dim;
   uint16_t *base = static_cast<uint16_t *>(cache->base) + per_tensor * 2 * layer;
   for (int which = 0; which < 2; ++which) {

@@ -12,9 +12,12 @@
 #include <memory>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "mi_attn.h"
+
+struct mi_kv_cache;
 
 namespace mi {
 
@@ -70,13 +73,13 @@ struct Context {
   std::vector<std::unique_ptr<ScratchPool>> pools;
   std::unordered_map<uintptr_t, Lease> leases;
   std::unordered_map<uintptr_t, size_t> tensors;  // mi_tensor_empty sizes
-  // Split-K arrival counters; zero between launches (the kernel's last
-  // workgroup resets its own counter).
-  uint32_t *counters = nullptr;
-  size_t counter_capacity = 0;
   bool profiling = false;
   std::vector<mi_kernel_profile> profiles;
   std::vector<FlashDecodeEntry> flash_decode;  // tuned table, sorted
+
+  // Live KV caches; destroying the context releases their storage and
+  // detaches them, so a cache destroyed later only frees its handle.
+  std::unordered_set<mi_kv_cache *> caches;
 };
 
 struct LaunchRecord {
@@ -99,9 +102,6 @@ struct Batch {
 mi_status scratch_alloc(Batch *batch, size_t bytes, void **out);
 mi_status scratch_free(Context *ctx, void *ptr);
 
-// Ensures at least `count` zeroed arrival counters exist. Growing drains
-// the stream first, since in-flight kernels may hold the old buffer.
-mi_status ensure_counters(Context *ctx, size_t count);
 
 // Launches through `fn` on the batch stream, bracketed by HIP events when
 // kernel profiling is on. `fn` returns the launch's hipError_t.

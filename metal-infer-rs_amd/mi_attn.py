@@ -484,9 +484,9 @@ class Batch:
         return stats
 
     def abandon(self) -> None:
-        if self.handle:
+        if self.handle and self.ctx.handle:
             lib().mi_batch_abandon(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

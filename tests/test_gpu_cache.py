@@ -149,6 +149,8 @@ def test_decode_loop_in_forward_layer_order(ctx):
         ref = oracle_attention(got_q, ctx.download(key.prefix(active)), vv, hq=hq, hkv=hkv, d=d,
                                off=offset)
         assert_parity(ctx.download(out), ref, label=f"step {step} kind {kind}")
-        assert np.abs(ctx.download(key.prefix(active)).astype(np.int32)
-                      - kk.astype(np.int32)).max() <= 1
+        # RoPE may cancel to near zero, so compare absolutely, scaled by the
+        # rows' magnitude (one f16 ulp at |x| < 4 is <= 2e-3).
+        got_k = f16(ctx.download(key.prefix(active))).astype(np.float64)
+        assert np.abs(got_k - f16(kk)).max() <= 2e-3 * max(1.0, np.abs(f16(kk)).max() / 4)
     cache.close()
