@@ -176,7 +176,8 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
     return MI_OK;
   }
   if (kind == MI_ATTN_FLASH_PREFILL && kernels::prefill_supported(p.D) &&
-      vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8)) {
+      vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8) &&
+      (out == nullptr || vector_friendly(*out, 4)) && (uint64_t)p.T * p.G < (1ull << 31)) {
     p.family = Family::Prefill;
     p.kernel = "attn_prefill";
     p.threads = 256;

@@ -212,3 +212,18 @@ def test_prefix_and_reshape():
         c.reshape((5, 5))
     with pytest.raises(MiError, match="contiguous"):
         t.reshape((4096, 1024))
+
+
+def test_flash_prefill_routes_to_mfma_kernel():
+    for d, expected in ((128, "attn_prefill"), (64, "attn_prefill"), (32, "attn_rows"),
+                        (256, "attn_rows")):
+        q, k = tensor((2048, 16, d)), tensor((2048, 8, d))
+        p = plan(q, k, k, AttentionConfig(16, 8, d, True, 0), FLASH_PREFILL)
+        assert p["kernel"] == expected, d
+    # c5: 4096 tokens x 8 heads per KV head = 256 row tiles of 128, one per KV head
+    q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
+    p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
+    assert p["kernel"] == "attn_prefill" and p["grid"][:2] == (256, 8)
+    # c3: 2048 x 2 = 4096 packed rows -> 32 row tiles per KV head
+    q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
+    assert plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)["grid"][:2] == (32, 8)

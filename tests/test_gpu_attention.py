@@ -103,6 +103,33 @@ def test_c3_prefill_seeded(ctx):
     _prefill_parity(ctx, c, "flash-prefill")
 
 
+def test_c5_chunked_prefill_seeded(ctx):
+    """4096 new tokens on a 16384-position cache, GQA 8:1; checked on 48 rows
+    (the first, the last and a seeded sample) against the oracle."""
+    c = workloads.case(5)
+    rng = np.random.default_rng(55)
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(c.tokens - 16, c.tokens),
+                                     rng.choice(c.tokens, 16, replace=False)]))
+    err = _prefill_parity(ctx, c, "flash-prefill", rows=rows)
+    print(f"c5 sampled rows max-abs {err:.2e}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1)])
+def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
+    rng = np.random.default_rng(hq * 100 + hkv + d)
+    for T, off, causal in ((1, 0, True), (7, 100, True), (100, 0, True), (300, 37, True),
+                           (65, 0, False), (129, 500, True)):
+        L = off + T if causal else T + 40
+        q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+        k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+        geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+        out = run_attention(ctx, q, k, v, kind="flash-prefill", causal=causal, **geo)
+        ref = oracle_attention(q, k, v, causal=causal, **geo)
+        assert_parity(out, ref, label=f"T={T} off={off} causal={causal}")
+
+
 def test_c4_batched_decode_seeded(ctx):
     """B=32 sequences, lengths ~ U[1024, 8192], one launch over all of them."""
     c = workloads.case(4)
