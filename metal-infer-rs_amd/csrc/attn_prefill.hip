@@ -15,6 +15,8 @@
 //    in which the S^T accumulator holds them;
 //  - the next tile's K/V global loads are in flight while the current tile
 //    is computed; causally heavy row tiles are dispatched first.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -52,9 +54,18 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// v_cvt_pk_f16_f32: two f32 -> packed f16, round to nearest even.
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
 }
+
+// O and l are rescaled only when a row's max grows past its reference by
+// more than 2^8. The reference may then lag the true max, which keeps
+// P = 2^(s - m_ref) <= 256 (well inside f16) and changes nothing in O / l,
+// since both use the same reference.
+constexpr float kRescaleLog2 = 8.0f;
 
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
@@ -109,23 +120,24 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   uint4 kreg[K_CHUNKS];
   uint4 vreg[V_PER][4];
   auto load_tile = [&](uint32_t j0) {
+    // Uniform tile base + 32-bit per-lane offsets (scalar-base addressing).
+    const uint16_t *kt = kbase + (int64_t)j0 * p.k_pos;
+    const uint16_t *vt = vbase + (int64_t)j0 * p.v_pos;
+    const int last = j0 + BN > kmax ? (int)(kmax - 1 - j0) : BN - 1;
 #pragma unroll
     for (int i = 0; i < K_CHUNKS; ++i) {
       const int c = tid + i * THREADS;
-      const int key = c / (D / 8), piece = c % (D / 8);
-      const uint32_t kk = min(j0 + key, kmax - 1);  // in bounds; masked later
-      kreg[i] = load16(kbase + (int64_t)kk * p.k_pos + piece * 8);
+      const int key = min(c / (D / 8), last);
+      kreg[i] = load16(kt + (uint32_t)(key * p.k_pos + (c % (D / 8)) * 8));
     }
 #pragma unroll
     for (int i = 0; i < V_PER; ++i) {
       const int job = tid + i * THREADS;
       if (job < V_JOBS) {
-        const int quad = job / (D / 8), dg = job % (D / 8);
+        const int quad = job % (BN / 4), dg = job / (BN / 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t kk = min(j0 + 4 * quad + e, kmax - 1);
-          vreg[i][e] = load16(vbase + (int64_t)kk * p.v_pos + dg * 8);
-        }
+        for (int e = 0; e < 4; ++e)
+          vreg[i][e] = load16(vt + (uint32_t)(min(4 * quad + e, last) * p.v_pos + dg * 8));
       }
     }
   };
@@ -140,7 +152,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     for (int i = 0; i < V_PER; ++i) {
       const int job = tid + i * THREADS;
       if (job < V_JOBS) {
-        const int quad = job / (D / 8), dg = job % (D / 8);
+        const int quad = job % (BN / 4), dg = job / (BN / 4);
         const int col = vt_col(4 * quad);
         const uint32_t *w0 = reinterpret_cast<const uint32_t *>(&vreg[i][0]);
         const uint32_t *w1 = reinterpret_cast<const uint32_t *>(&vreg[i][1]);
@@ -167,10 +179,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   float l_run = 0.0f;       // this half-wave's share of the row sum
   const float c2 = p.scale_log2;
 
-  load_tile(0);
-  store_tile();
-  __syncthreads();
-  for (uint32_t it = 0; it < n_tiles; ++it) {
+  auto step = [&](uint32_t it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const uint32_t j0 = it * BN;
     const bool more = it + 1 < n_tiles;
     if (more) load_tile(j0 + BN);
@@ -188,23 +198,37 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[c], s[mt], 0, 0, 0);
       }
     }
-    // Online softmax of row n over this lane's 32 keys.
+    // Online softmax of row n over this lane's 32 keys (MASK: causal and
+    // length mask, needed only past the first row's window).
+    int lim_rel = BN;
+    if constexpr (MASK)
+      lim_rel = (int)max(min((int64_t)lim - (int64_t)j0, (int64_t)BN), (int64_t)-1);
     float mx = -INFINITY;
-    const bool masked = (uint64_t)j0 + BN - 1 > full_lim;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        if (masked) {
-          const uint64_t key = j0 + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (key > lim) s[mt][r] = -INFINITY;
+        if constexpr (MASK) {
+          const int key_rel = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+          s[mt][r] = key_rel > lim_rel ? -INFINITY : s[mt][r];
         }
         mx = fmaxf(mx, s[mt][r]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);  // finite: key 0 is visible to all
-    const float alpha = exp2_raw((m_run - m_new) * c2);
-    const float mc = m_new * c2;
+    // m_run is the reference max; it only moves when some row of the wave
+    // outgrows it by 2^kRescaleLog2 (always on the first tile, as key 0 is
+    // visible to every row).
+    if (__any((mx - m_run) * c2 > kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = exp2_raw((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run * c2;
     uint32_t pw[2][8];  // P as packed f16 pairs, in accumulator order
     float psum = 0.0f;
 #pragma unroll
@@ -216,14 +240,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
         const uint32_t w = pack_f16x2(p0, p1);
         pw[mt][r >> 1] = w;
         // The row sum uses the same f16-rounded weights as P V.
-        psum += lo_f16(w) + hi_f16(w);
+        psum = dot2(w, 0x3c003c00u, psum);
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    l_run += psum;
 
     // O^T[d][row] += V^T[d][keys] P^T[keys][row], four 16-key chunks.
 #pragma unroll
@@ -243,7 +262,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
       store_tile();
       __syncthreads();
     }
-  }
+  };
+
+  // Tiles wholly inside the first row's window need no mask.
+  const uint32_t n_full = (uint32_t)min((uint64_t)n_tiles, (full_lim + 1) / BN);
+  load_tile(0);
+  store_tile();
+  __syncthreads();
+  uint32_t it = 0;
+  for (; it < n_full; ++it) step(it, std::false_type{});
+  for (; it < n_tiles; ++it) step(it, std::true_type{});
 
   // Normalise and store: lane (h, n) holds d = 32dt + 8q + 4h + 0..3.
   const float l_total = l_run + __shfl_xor(l_run, 32, 64);
