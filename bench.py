@@ -110,30 +110,79 @@ def time_graph(hip: Hip, exe, stream, reps: int) -> float:
     return ms.value / 1e3 / reps
 
 
-def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, float]:
-    """Average duration (s) of the dominant kernel over `count` eager calls,
-    from HIP events placed around each launch on the batch's stream."""
+def time_eager(ctx: mi_attn.Context, hip: Hip, enqueue, steps: int) -> float:
+    """Seconds per call of `steps` eager calls in one batch, bracketed by
+    events on the library stream (used under rocprofv3, which cannot trace
+    graph launches here)."""
+    batch = ctx.begin_batch()
+    stream = ctypes.c_void_p(batch.stream)
+    start, end = hip.event(), hip.event()
+    hip.check(hip.lib.hipStreamSynchronize(stream), "sync")
+    hip.check(hip.lib.hipEventRecord(start, stream), "record")
+    keep = [enqueue(batch, i) for i in range(steps)]
+    hip.check(hip.lib.hipEventRecord(end, stream), "record")
+    batch.finish()
+    hip.check(hip.lib.hipEventSynchronize(end), "sync")
+    ms = ctypes.c_float()
+    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, end), "elapsed")
+    hip.lib.hipEventDestroy(start)
+    hip.lib.hipEventDestroy(end)
+    del keep
+    return ms.value / 1e3 / steps
+
+
+def timed(ctx, hip, enqueue, steps: int, eager: bool, reps: int) -> tuple[int, float]:
+    """(calls timed, seconds per call): a HIP graph of `steps` calls replayed
+    `reps` times, or `steps * reps` eager calls."""
+    if eager:
+        return steps * reps, time_eager(ctx, hip, enqueue, steps * reps)
+    exe, graph, stream, _ = capture(hip, ctx, enqueue, steps)
+    time_graph(hip, exe, stream, 1)
+    seconds = time_graph(hip, exe, stream, reps) / steps
+    hip.lib.hipGraphExecDestroy(exe)
+    hip.lib.hipGraphDestroy(graph)
+    return steps * reps, seconds
+
+
+def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, float, dict]:
+    """The dominant kernel (largest total time) of `count` eager calls, its
+    average duration per launch (s), and every kernel's average, from HIP
+    events placed around each launch on the batch's stream."""
     ctx.take_kernel_profiles()
     ctx.set_kernel_profiling(True)
     try:
-        for i in range(count):
-            batch = ctx.begin_batch()
-            enqueue(batch, i)
-            batch.finish()
+        # Back to back in one batch, as in the timed region.
+        batch = ctx.begin_batch()
+        keep = [enqueue(batch, i) for i in range(count)]
+        batch.finish()
+        del keep
         profiles = ctx.take_kernel_profiles()
     finally:
         ctx.set_kernel_profiling(False)
     by_name: dict[str, list[float]] = {}
     for name, ns in profiles:
         by_name.setdefault(name, []).append(ns)
+    average = {n: sum(v) / len(v) * 1e-9 for n, v in by_name.items()}
     name = max(by_name, key=lambda n: sum(by_name[n]))
-    per_call = sum(sum(v) for v in by_name.values()) / count
-    return name, per_call * 1e-9
+    return name, average[name], average
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel
+    calibration recorded there), or None when not measured."""
+    path = ROOT / "profiles" / "pmc_traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("workloads", {}).get(workload, {})
+    if entry.get("kernel") != kernel:
+        return None
+    return entry.get("traffic_bytes")
 
 
 # ----------------------------------------------------------------- decode --
 
-def bench_decode(ctx, hip, steps, warmup):
+def bench_decode(ctx, hip, steps, warmup, eager):
     c = workloads.case(2)
     hq, hkv, d, L = c.q_heads, c.kv_heads, c.head_dim, c.kv_length
     log(f"decode c2: {ROTATE} head-major caches of {L} positions")
@@ -155,20 +204,15 @@ def bench_decode(ctx, hip, steps, warmup):
         enqueue(b, i)
         b.finish()
     per_graph = max(ROTATE, (steps // ROTATE) * ROTATE)
-    exe, graph, stream, _ = capture(hip, ctx, enqueue, per_graph)
-    time_graph(hip, exe, stream, 1)
-    reps = max(1, steps // per_graph)
-    seconds = time_graph(hip, exe, stream, reps) / per_graph
-    hip.lib.hipGraphExecDestroy(exe)
-    hip.lib.hipGraphDestroy(graph)
-    name, kernel_s = kernel_profile(ctx, enqueue, ROTATE)
+    calls, seconds = timed(ctx, hip, enqueue, per_graph, eager, max(1, steps // per_graph))
+    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 4 * ROTATE)
     nbytes = c.algorithmic_bytes()
     cache.close()
-    return c, dict(steps=per_graph * reps, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   bytes=nbytes)
+    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
+                   kernels=kernels, bytes=nbytes)
 
 
-def bench_batched_decode(ctx, hip, steps):
+def bench_batched_decode(ctx, hip, steps, eager):
     c = workloads.case(4)
     B, hq, hkv, d, cap = c.batch, c.q_heads, c.kv_heads, c.head_dim, c.kv_length
     log(f"batched decode c4: B={B}, sum L={int(c.lengths.sum())}")
@@ -192,17 +236,13 @@ def bench_batched_decode(ctx, hip, steps):
         b = ctx.begin_batch()
         enqueue(b, i)
         b.finish()
-    exe, graph, stream, _ = capture(hip, ctx, enqueue, steps)
-    time_graph(hip, exe, stream, 1)
-    seconds = time_graph(hip, exe, stream, 3) / steps
-    hip.lib.hipGraphExecDestroy(exe)
-    hip.lib.hipGraphDestroy(graph)
-    name, kernel_s = kernel_profile(ctx, enqueue, 5)
-    return c, dict(steps=steps * 3, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   bytes=c.algorithmic_bytes())
+    calls, seconds = timed(ctx, hip, enqueue, steps, eager, 3)
+    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 10)
+    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
+                   kernels=kernels, bytes=c.algorithmic_bytes())
 
 
-def bench_prefill(ctx, hip, config, steps):
+def bench_prefill(ctx, hip, config, steps, eager):
     c = workloads.case(config)
     hq, hkv, d = c.q_heads, c.kv_heads, c.head_dim
     log(f"prefill c{config}: T={c.tokens} L={c.kv_length} Hq={hq} Hkv={hkv}")
@@ -221,15 +261,12 @@ def bench_prefill(ctx, hip, config, steps):
     b = ctx.begin_batch()
     enqueue(b, 0)
     b.finish()
-    exe, graph, stream, _ = capture(hip, ctx, enqueue, steps)
-    time_graph(hip, exe, stream, 1)
-    seconds = time_graph(hip, exe, stream, 2) / steps
-    hip.lib.hipGraphExecDestroy(exe)
-    hip.lib.hipGraphDestroy(graph)
-    name, kernel_s = kernel_profile(ctx, enqueue, 3)
+    calls, seconds = timed(ctx, hip, enqueue, steps, eager, 2)
+    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 10 if config == 3 else 3)
     cache.close()
-    return c, dict(steps=steps * 2, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   flops=c.flops(), plan=ctx.plan(q, key, value, cfg, kind)["kernel"])
+    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
+                   kernels=kernels, flops=c.flops(),
+                   plan=ctx.plan(q, key, value, cfg, kind)["kernel"])
 
 
 # -------------------------------------------------------------- CPU leg ---
@@ -256,85 +293,120 @@ def cpu_baseline(decode_case) -> dict:
                       f"{seconds * 1e3:.2f} ms each, {threads} OpenMP threads"}
 
 
+def hbm_roofline(nbytes: int, run: dict, workload: str) -> dict:
+    achieved = nbytes / run["kernel_s"] / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(workload, run["kernel"]), "kernel": run["kernel"],
+            "kernel_us": round(run["kernel_s"] * 1e6, 3), "algorithmic_bytes": nbytes,
+            "kernels_us": {n: round(t * 1e6, 3) for n, t in run["kernels"].items()}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--workloads", default="c2,c4,c3,c5",
+                    help="comma list of c2 (headline decode), c4, c3, c5; profiling runs "
+                         "select one at a time")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of HIP graph replays (for rocprofv3)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB KV copy (PMC traffic calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the attention path has no multi-GPU "
               "component in this build (see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
+    chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
+    unknown = set(chosen) - {"c2", "c3", "c4", "c5"}
+    if unknown:
+        print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
+        return 2
 
     hip = Hip()
     ctx = mi_attn.Context(0)
     log(f"device: {ctx.device_name}, {ctx.compute_units} CUs")
-    dc, dec = bench_decode(ctx, hip, args.steps, args.warmup)
-    value = dec["bytes"] / dec["seconds"] / 1e9
-    achieved = dec["bytes"] / dec["kernel_s"] / 1e9
-    log(f"decode: {value:.1f} GB/s whole-job, kernel {dec['kernel']} "
-        f"{dec['kernel_s'] * 1e6:.2f} us -> {achieved:.1f} GB/s")
-    result = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": dec["steps"],
-        "warmup": args.warmup,
-        "ms_per_step": round(dec["seconds"] * 1e3, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic: seeded XorShift64/Box-Muller N(0,1) f16 (BASELINE configs)",
-        "config": {"workload": "c2 single-token decode, L=2048, Hq=16, Hkv=8, D=128, "
-                               f"head-major fp16 cache, {ROTATE} rotated caches, HIP graph",
-                   "kv_length": dc.kv_length, "q_heads": dc.q_heads, "kv_heads": dc.kv_heads,
-                   "head_dim": dc.head_dim},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": dec["kernel"],
-                     "kernel_us": round(dec["kernel_s"] * 1e6, 3),
-                     "algorithmic_bytes": dec["bytes"]},
-    }
-    if not args.decode_only:
-        bc, bat = bench_batched_decode(ctx, hip, 20)
+    timing = "eager launches" if args.eager else "HIP graph replay"
+    result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": 0,
+              "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+              "data": "synthetic: seeded XorShift64/Box-Muller N(0,1) f16 (BASELINE configs)"}
+    dc = None
+    if "c2" in chosen:
+        dc, dec = bench_decode(ctx, hip, args.steps, args.warmup, args.eager)
+        value = dec["bytes"] / dec["seconds"] / 1e9
+        roof = hbm_roofline(dec["bytes"], dec, "c2")
+        log(f"decode: {value:.1f} GB/s whole-job, kernel {dec['kernel']} "
+            f"{dec['kernel_s'] * 1e6:.2f} us -> {roof['achieved']:.1f} GB/s")
+        result.update({
+            "value": round(value, 2), "steps": dec["steps"],
+            "ms_per_step": round(dec["seconds"] * 1e3, 6),
+            "config": {"workload": "c2 single-token decode, L=2048, Hq=16, Hkv=8, D=128, "
+                                   f"head-major fp16 cache, {ROTATE} rotated caches, {timing}",
+                       "kv_length": dc.kv_length, "q_heads": dc.q_heads,
+                       "kv_heads": dc.kv_heads, "head_dim": dc.head_dim},
+            "roofline": roof})
+    else:
+        log("c2 not selected: the headline fields stay null (profiling run)")
+    if "c4" in chosen:
+        bc, bat = bench_batched_decode(ctx, hip, 20, args.eager)
         bval = bat["bytes"] / bat["seconds"] / 1e9
-        bach = bat["bytes"] / bat["kernel_s"] / 1e9
         log(f"batched decode: {bval:.1f} GB/s, kernel {bat['kernel_s'] * 1e6:.1f} us")
         result["batched_decode"] = {
             "workload": "c4 batched decode B=32, L~U[1024,8192] seeded, Hq=32, Hkv=8, D=128",
             "value": round(bval, 2), "unit": "GB/s", "ms_per_step": round(bat["seconds"] * 1e3, 4),
-            "roofline": {"bound": "hbm", "achieved": round(bach, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(bach / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": bat["kernel"], "algorithmic_bytes": bat["bytes"]}}
-        prefill = []
-        for config, steps in ((3, 10), (5, 2)):
-            if config == 5 and not mi_attn_prefill_is_mfma(ctx):
-                log("c5 skipped: FlashPrefill is not on the MFMA kernel in this build")
-                continue
-            pc, pre = bench_prefill(ctx, hip, config, steps)
-            tflops = pre["flops"] / pre["seconds"] / 1e12
-            kt = pre["flops"] / pre["kernel_s"] / 1e12
-            log(f"prefill c{config}: {tflops:.1f} TFLOP/s, kernel {pre['kernel_s'] * 1e3:.3f} ms")
-            prefill.append({"workload": pc.description, "value": round(tflops, 2),
-                            "unit": "TFLOP/s", "ms_per_step": round(pre["seconds"] * 1e3, 4),
-                            "kernel_family": pre["plan"],
-                            "roofline": {"bound": "mfma", "achieved": round(kt, 2),
-                                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                         "frac": round(kt / MFMA_F16_PEAK_TFLOPS, 4),
-                                         "traffic": None, "kernel": pre["kernel"],
-                                         "algorithmic_flops": pre["flops"]}})
+            "roofline": hbm_roofline(bat["bytes"], bat, "c4")}
+    prefill = []
+    for config, steps in ((3, 10), (5, 2)):
+        if f"c{config}" not in chosen:
+            continue
+        if config == 5 and not mi_attn_prefill_is_mfma(ctx):
+            log("c5 skipped: FlashPrefill is not on the MFMA kernel in this build")
+            continue
+        pc, pre = bench_prefill(ctx, hip, config, steps, args.eager)
+        tflops = pre["flops"] / pre["seconds"] / 1e12
+        kt = pre["flops"] / pre["kernel_s"] / 1e12
+        log(f"prefill c{config}: {tflops:.1f} TFLOP/s, kernel {pre['kernel_s'] * 1e3:.3f} ms")
+        prefill.append({"workload": pc.description, "value": round(tflops, 2),
+                        "unit": "TFLOP/s", "ms_per_step": round(pre["seconds"] * 1e3, 4),
+                        "kernel_family": pre["plan"],
+                        "roofline": {"bound": "mfma", "achieved": round(kt, 2),
+                                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(kt / MFMA_F16_PEAK_TFLOPS, 4),
+                                     "traffic": measured_traffic(f"c{config}", pre["kernel"]),
+                                     "kernel": pre["kernel"],
+                                     "kernel_ms": round(pre["kernel_s"] * 1e3, 4),
+                                     "algorithmic_flops": pre["flops"]}})
+    if prefill:
         result["prefill"] = prefill
-    if not args.no_cpu:
+    if args.copy_calibration:
+        result["copy_calibration"] = copy_calibration(ctx, hip)
+    if not args.no_cpu and dc is not None:
         log("cpu baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline(dc)
     print(json.dumps(result), flush=True)
     ctx.close()
     return 0
+
+
+def copy_calibration(ctx, hip) -> dict:
+    """A plain copy of known size (copy_kv_kernel: 256 MiB read, 256 MiB
+    written), run three times; its FETCH_SIZE / WRITE_SIZE readings scale the
+    counters of the attention kernels to bytes."""
+    hkv, d, positions = 8, 128, 131072
+    nbytes = positions * hkv * d * 2
+    cache = ctx.kv_cache(1, hkv, d, positions)
+    key, _ = cache.layer(0)
+    source = ctx.empty((positions, hkv, d))
+    calls, seconds = timed(ctx, hip, lambda b, i: b.copy_into_cache(source, key, 0), 3, True, 1)
+    source.free()
+    cache.close()
+    log(f"copy calibration: {nbytes} B read + written, {seconds * 1e6:.1f} us per copy")
+    return {"kernel": "copy_kv", "bytes_read": nbytes, "bytes_written": nbytes, "calls": calls,
+            "us_per_copy": round(seconds * 1e6, 2)}
 
 
 def mi_attn_prefill_is_mfma(ctx) -> bool:

@@ -67,6 +67,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 // since both use the same reference.
 constexpr float kRescaleLog2 = 8.0f;
 
+// sched_group_barrier instruction classes (LLVM AMDGPU): MFMA, LDS read.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kReadAhead = 4;
+
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     const PrefillParams p) {
@@ -77,15 +82,32 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   constexpr int K_CHUNKS = BN * D / 8 / THREADS;           // 16-B pieces
   constexpr int V_JOBS = (BN / 4) * (D / 8);                // 4 keys x 8 d
   constexpr int V_PER = (V_JOBS + THREADS - 1) / THREADS;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * VS];
+  // Two LDS stages: tile i is read from one while tile i+1 is written into
+  // the other, so one barrier per tile suffices.
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds2[2][BN * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds2[2][D * VS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
   const uint32_t G = p.group;
-  const uint32_t tile = p.row_tiles - 1 - blockIdx.x;  // heavy tiles first
-  const uint32_t kvh = blockIdx.y;
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
+  // by linear id, so id % 8 selects the XCD. When the KV heads split evenly
+  // over the XCDs, each XCD gets whole heads (their K/V stay in its L2);
+  // within an XCD the heaviest row tiles go first.
+  uint32_t tile, kvh;
+  {
+    const uint32_t id = blockIdx.x + gridDim.x * blockIdx.y;
+    const uint32_t H = gridDim.y;
+    if (H % 8 == 0) {
+      const uint32_t xcd = id % 8, k = id / 8, per = H / 8;
+      kvh = xcd * per + k % per;
+      tile = p.row_tiles - 1 - k / per;
+    } else {
+      tile = p.row_tiles - 1 - blockIdx.x;
+      kvh = blockIdx.y;
+    }
+  }
   const uint32_t row0 = tile * BM;
   const uint32_t my_row = row0 + wave * 32 + n;
   const uint32_t my_t = my_row / G, my_g = my_row % G;
@@ -141,7 +163,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
       }
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int stage) {
+    uint16_t *k_lds = k_lds2[stage];
+    uint16_t *v_lds = v_lds2[stage];
 #pragma unroll
     for (int i = 0; i < K_CHUNKS; ++i) {
       const int c = tid + i * THREADS;
@@ -182,10 +206,13 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   auto step = [&](uint32_t it, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const uint32_t j0 = it * BN;
-    const bool more = it + 1 < n_tiles;
-    if (more) load_tile(j0 + BN);
+    const uint16_t *k_lds = k_lds2[it & 1];
+    const uint16_t *v_lds = v_lds2[it & 1];
 
-    // S^T[key][row] for the 64 keys of the tile: two 32-key M tiles.
+    // S^T[key][row] for the 64 keys of the tile: two 32-key M tiles. MFMA
+    // phases run at raised wave priority, so while one wave of a SIMD feeds
+    // the matrix core the other's softmax VALU fills the issue gaps.
+    __builtin_amdgcn_s_setprio(1);
     float16_t s[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -198,6 +225,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[c], s[mt], 0, 0, 0);
       }
     }
+    // Schedule: kReadAhead operand reads stay in flight ahead of the MFMAs
+    // (one wave streams at most one 1 KB LDS operand per MFMA duration).
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadAhead, 0);
+#pragma unroll
+    for (int k = 0; k < 2 * DC - kReadAhead; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 0);
+    __builtin_amdgcn_s_setprio(0);
     // Online softmax of row n over this lane's 32 keys (MASK: causal and
     // length mask, needed only past the first row's window).
     int lim_rel = BN;
@@ -245,6 +282,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     l_run += psum;
 
     // O^T[d][row] += V^T[d][keys] P^T[keys][row], four 16-key chunks.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int mt = c >> 1, base = (c & 1) * 4;
@@ -257,17 +295,27 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[dt], 0, 0, 0);
       }
     }
-    __syncthreads();  // every wave is done reading this tile
-    if (more) {
-      store_tile();
-      __syncthreads();
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadAhead, 1);
+#pragma unroll
+    for (int k = 0; k < 4 * DT - kReadAhead; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 1);
     }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 1);
+    __builtin_amdgcn_s_setprio(0);
+    // Tile it+1 (loaded during the previous tile) goes to the other stage,
+    // whose last readers finished before the previous barrier; then the
+    // loads for tile it+2 are issued to overlap the next tile's compute.
+    if (it + 1 < n_tiles) store_tile((it + 1) & 1);
+    __syncthreads();
+    if (it + 2 < n_tiles) load_tile(j0 + 2 * BN);
   };
 
   // Tiles wholly inside the first row's window need no mask.
   const uint32_t n_full = (uint32_t)min((uint64_t)n_tiles, (full_lim + 1) / BN);
   load_tile(0);
-  store_tile();
+  store_tile(0);
+  if (n_tiles > 1) load_tile(BN);
   __syncthreads();
   uint32_t it = 0;
   for (; it < n_full; ++it) step(it, std::false_type{});
@@ -296,20 +344,13 @@ bool prefill_supported(uint32_t head_dim) {
   return head_dim == 64 || head_dim == 128;
 }
 
-hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim,
-                          hipStream_t stream) {
+hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
   const dim3 grid(p.row_tiles, p.kv_heads);
   switch (head_dim) {
-    case 64:
-      attn_prefill_kernel<64><<<grid, THREADS, 0, stream>>>(p);
-      break;
-    case 128:
-      attn_prefill_kernel<128><<<grid, THREADS, 0, stream>>>(p);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case 64: return dispatch(attn_prefill_kernel<64>, grid, dim3(THREADS), 0, l, p);
+    case 128: return dispatch(attn_prefill_kernel<128>, grid, dim3(THREADS), 0, l, p);
+    default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace kernels

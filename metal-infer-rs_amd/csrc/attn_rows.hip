@@ -366,34 +366,34 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const RowsParams p) {
 }
 
 template <int D, int WAVES, int GC>
-hipError_t launch_rows_dwg(const RowsParams &p, hipStream_t stream) {
-  const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
-                  p.batch * p.tokens);
-  attn_rows_kernel<D, WAVES, GC><<<grid, WAVES * 64, 0, stream>>>(p);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || p.max_splits <= 1) return err;
+hipError_t launch_rows_dwg(const RowsParams &p, RowsPhase phase, const Launch &l) {
+  if (phase == RowsPhase::Split) {
+    const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
+                    p.batch * p.tokens);
+    return dispatch(attn_rows_kernel<D, WAVES, GC>, grid, dim3(WAVES * 64), 0, l, p);
+  }
+  if (p.max_splits <= 1) return no_dispatch(l);
   const uint32_t units = p.batch * p.tokens * p.kv_heads * p.head_chunks;
-  attn_merge_kernel<D, GC><<<units, 256, 0, stream>>>(p);
-  return hipGetLastError();
+  return dispatch(attn_merge_kernel<D, GC>, dim3(units), dim3(256), 0, l, p);
 }
 
 template <int D, int WAVES>
-hipError_t launch_rows_dw(const RowsParams &p, uint32_t chunk,
-                          hipStream_t stream) {
+hipError_t launch_rows_dw(const RowsParams &p, uint32_t chunk, RowsPhase phase,
+                          const Launch &l) {
   switch (chunk) {
-    case 8: return launch_rows_dwg<D, WAVES, 8>(p, stream);
-    case 4: return launch_rows_dwg<D, WAVES, 4>(p, stream);
-    case 2: return launch_rows_dwg<D, WAVES, 2>(p, stream);
-    case 1: return launch_rows_dwg<D, WAVES, 1>(p, stream);
+    case 8: return launch_rows_dwg<D, WAVES, 8>(p, phase, l);
+    case 4: return launch_rows_dwg<D, WAVES, 4>(p, phase, l);
+    case 2: return launch_rows_dwg<D, WAVES, 2>(p, phase, l);
+    case 1: return launch_rows_dwg<D, WAVES, 1>(p, phase, l);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int D>
 hipError_t launch_rows_d(const RowsParams &p, uint32_t waves, uint32_t chunk,
-                         hipStream_t stream) {
-  if (waves == 4) return launch_rows_dw<D, 4>(p, chunk, stream);
-  if (waves == 2) return launch_rows_dw<D, 2>(p, chunk, stream);
+                         RowsPhase phase, const Launch &l) {
+  if (waves == 4) return launch_rows_dw<D, 4>(p, chunk, phase, l);
+  if (waves == 2) return launch_rows_dw<D, 2>(p, chunk, phase, l);
   return hipErrorInvalidValue;
 }
 
@@ -405,17 +405,17 @@ uint32_t rows_chunk(uint32_t group) {
 }
 
 hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
-                       uint32_t chunk, hipStream_t stream) {
+                       uint32_t chunk, RowsPhase phase, const Launch &l) {
   switch (head_dim) {
-    case 1: return launch_rows_d<1>(p, waves, chunk, stream);
-    case 2: return launch_rows_d<2>(p, waves, chunk, stream);
-    case 4: return launch_rows_d<4>(p, waves, chunk, stream);
-    case 8: return launch_rows_d<8>(p, waves, chunk, stream);
-    case 16: return launch_rows_d<16>(p, waves, chunk, stream);
-    case 32: return launch_rows_d<32>(p, waves, chunk, stream);
-    case 64: return launch_rows_d<64>(p, waves, chunk, stream);
-    case 128: return launch_rows_d<128>(p, waves, chunk, stream);
-    case 256: return launch_rows_d<256>(p, waves, chunk, stream);
+    case 1: return launch_rows_d<1>(p, waves, chunk, phase, l);
+    case 2: return launch_rows_d<2>(p, waves, chunk, phase, l);
+    case 4: return launch_rows_d<4>(p, waves, chunk, phase, l);
+    case 8: return launch_rows_d<8>(p, waves, chunk, phase, l);
+    case 16: return launch_rows_d<16>(p, waves, chunk, phase, l);
+    case 32: return launch_rows_d<32>(p, waves, chunk, phase, l);
+    case 64: return launch_rows_d<64>(p, waves, chunk, phase, l);
+    case 128: return launch_rows_d<128>(p, waves, chunk, phase, l);
+    case 256: return launch_rows_d<256>(p, waves, chunk, phase, l);
     default: return hipErrorInvalidValue;
   }
 }

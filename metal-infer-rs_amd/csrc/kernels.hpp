@@ -3,11 +3,40 @@
 // read has a unit innermost stride.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace mi {
 namespace kernels {
+
+// Where a kernel runs: its stream, and optionally start / stop events that
+// hipExtLaunchKernelGGL binds to the dispatch packet itself, so they time
+// the kernel's execution without the enqueue latency that separate
+// hipEventRecord markers would add.
+struct Launch {
+  hipStream_t stream = nullptr;
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+
+template <typename... Params, typename... Args>
+hipError_t dispatch(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t lds,
+                    const Launch &l, Args... args) {
+  if (l.start == nullptr && l.stop == nullptr)
+    kernel<<<grid, block, lds, l.stream>>>(args...);
+  else
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, l.stream, l.start, l.stop, 0, args...);
+  return hipGetLastError();
+}
+
+// A launcher with nothing to run still stamps its events, so a profiled
+// launch record always has both.
+inline hipError_t no_dispatch(const Launch &l) {
+  if (l.start != nullptr) hipEventRecord(l.start, l.stream);
+  if (l.stop != nullptr) hipEventRecord(l.stop, l.stream);
+  return hipGetLastError();
+}
 
 // Split-K "rows" attention: one workgroup per (sequence*token, KV head,
 // head chunk, key split). Serves Tiled, DecodeSplitKv, FlashDecode and the
@@ -91,8 +120,12 @@ struct PrefillParams {
   float scale_log2;
 };
 
+// Split pass (one workgroup per key block; writes the output directly when a
+// row has one block) and merge pass (combines the partials of rows with more
+// than one block; no launch when max_splits <= 1). Same stream, in order.
+enum class RowsPhase { Split, Merge };
 hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
-                       uint32_t chunk, hipStream_t stream);
+                       uint32_t chunk, RowsPhase phase, const Launch &l);
 // Largest head chunk (of 8, 4, 2, 1) that divides `group`.
 uint32_t rows_chunk(uint32_t group);
 
@@ -100,18 +133,17 @@ uint32_t rows_chunk(uint32_t group);
 // (token, head) grid. Scores of up to kNaiveLdsKeys keys live in LDS; longer
 // rows spill to NaiveParams::scores, which must hold row_count * L floats.
 hipError_t launch_naive(const NaiveParams &p, uint32_t row_begin,
-                        uint32_t row_count, hipStream_t stream);
+                        uint32_t row_count, const Launch &l);
 constexpr uint32_t kNaiveLdsKeys = 12288;
 
-hipError_t launch_copy_kv(const CopyKvParams &p, hipStream_t stream);
-hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, hipStream_t stream);
+hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l);
+hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l);
 
 // Rows of the packed (token, head-in-group) M dimension per prefill
 // workgroup.
 constexpr uint32_t kPrefillBlockM = 128;
 bool prefill_supported(uint32_t head_dim);
-hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim,
-                          hipStream_t stream);
+hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
 
 }  // namespace kernels
 }  // namespace mi

@@ -217,9 +217,13 @@ mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
   rp.max_splits = p.splits;
   rp.head_chunks = p.G / p.chunk;
   rp.group = p.G;
-  st = launch(batch, p.kernel, [&](hipStream_t s) {
-    return kernels::launch_rows(rp, p.D, p.waves, p.chunk, s);
+  st = launch(batch, p.kernel, [&](const kernels::Launch &s) {
+    return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Split, s);
   });
+  if (st == MI_OK && p.splits > 1)
+    st = launch(batch, "attn_merge", [&](const kernels::Launch &s) {
+      return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Merge, s);
+    });
   // In-order execution makes the range reusable by later work of the batch.
   if (scratch != nullptr) scratch_free(ctx, scratch);
   return st;
@@ -264,7 +268,7 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     for (uint32_t begin = 0; begin < rows && st == MI_OK; begin += chunk_rows) {
       const uint32_t count = std::min(chunk_rows, rows - begin);
       st = launch(batch, p.kernel,
-                  [&](hipStream_t s) { return kernels::launch_naive(np, begin, count, s); });
+                  [&](const kernels::Launch &s) { return kernels::launch_naive(np, begin, count, s); });
     }
     if (scores != nullptr) scratch_free(batch->ctx, scores);
     return st;
@@ -280,7 +284,7 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     pp.row_tiles = p.grid[0];
     pp.scale_log2 = scale * log2e;
     return launch(batch, p.kernel,
-                  [&](hipStream_t s) { return kernels::launch_prefill(pp, p.D, s); });
+                  [&](const kernels::Launch &s) { return kernels::launch_prefill(pp, p.D, s); });
   }
   kernels::RowsParams rp{};
   rp.q = qd, rp.q_seq = 0, rp.q_tok = q->stride[0], rp.q_head = q->stride[1];
@@ -525,7 +529,7 @@ mi_status mi_copy_into_cache(mi_batch *batch, const mi_tensor *source, const mi_
   cp.d_pos = cache->stride[0], cp.d_head = cache->stride[1];
   cp.heads = (uint32_t)source->shape[1];
   cp.head_dim = (uint32_t)source->shape[2];
-  return launch(batch, "copy_kv", [&](hipStream_t s) { return kernels::launch_copy_kv(cp, s); });
+  return launch(batch, "copy_kv", [&](const kernels::Launch &s) { return kernels::launch_copy_kv(cp, s); });
 }
 
 mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
@@ -576,7 +580,7 @@ mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q, const mi_te
   qp.cache = static_cast<uint16_t *>(key_cache->data);
   qp.c_pos = key_cache->stride[0], qp.c_head = key_cache->stride[1];
   return launch(batch, "qk_norm_rope_cache",
-                [&](hipStream_t s) { return kernels::launch_qk_norm_rope(qp, s); });
+                [&](const kernels::Launch &s) { return kernels::launch_qk_norm_rope(qp, s); });
 }
 
 }  // extern "C"

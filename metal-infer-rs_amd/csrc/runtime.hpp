@@ -15,6 +15,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "kernels.hpp"
 #include "mi_attn.h"
 
 struct mi_kv_cache;
@@ -103,27 +104,26 @@ mi_status scratch_alloc(Batch *batch, size_t bytes, void **out);
 mi_status scratch_free(Context *ctx, void *ptr);
 
 
-// Launches through `fn` on the batch stream, bracketed by HIP events when
-// kernel profiling is on. `fn` returns the launch's hipError_t.
+// Launches through `fn` on the batch stream. With kernel profiling on, the
+// launch carries start / stop events bound to the kernel's dispatch (see
+// kernels::Launch). `fn` returns the launch's hipError_t.
 template <typename Fn>
 mi_status launch(Batch *batch, const char *kernel, Fn &&fn) {
-  hipEvent_t start = nullptr, end = nullptr;
+  kernels::Launch l;
+  l.stream = batch->ctx->stream;
   if (batch->ctx->profiling) {
-    if (hipEventCreate(&start) != hipSuccess ||
-        hipEventCreate(&end) != hipSuccess)
+    if (hipEventCreate(&l.start) != hipSuccess || hipEventCreate(&l.stop) != hipSuccess) {
+      if (l.start) hipEventDestroy(l.start);
       return fail(MI_ERR_PROFILING, "could not create profiling events");
-    hipEventRecord(start, batch->ctx->stream);
+    }
   }
-  hipError_t err = fn(batch->ctx->stream);
+  hipError_t err = fn(l);
   if (err != hipSuccess) {
-    if (start) hipEventDestroy(start);
-    if (end) hipEventDestroy(end);
+    if (l.start) hipEventDestroy(l.start);
+    if (l.stop) hipEventDestroy(l.stop);
     return hip_fail(MI_ERR_PIPELINE, kernel, err);
   }
-  if (start) {
-    hipEventRecord(end, batch->ctx->stream);
-    batch->launches.push_back({kernel, start, end});
-  }
+  if (l.start) batch->launches.push_back({kernel, l.start, l.stop});
   return MI_OK;
 }
 

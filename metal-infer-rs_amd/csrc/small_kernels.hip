@@ -138,15 +138,14 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(QkNormRopeParams p) {
 }  // namespace
 
 hipError_t launch_naive(const NaiveParams &p, uint32_t row_begin,
-                        uint32_t row_count, hipStream_t stream) {
-  if (row_count == 0) return hipSuccess;
-  const size_t lds =
-      p.kv_length <= kNaiveLdsKeys ? (size_t)p.kv_length * sizeof(float) : 0;
-  attn_naive_kernel<<<row_count, 256, lds, stream>>>(p, row_begin);
-  return hipGetLastError();
+                        uint32_t row_count, const Launch &l) {
+  if (row_count == 0) return no_dispatch(l);
+  const uint32_t lds =
+      p.kv_length <= kNaiveLdsKeys ? p.kv_length * (uint32_t)sizeof(float) : 0;
+  return dispatch(attn_naive_kernel, dim3(row_count), dim3(256), lds, l, p, row_begin);
 }
 
-hipError_t launch_copy_kv(const CopyKvParams &p, hipStream_t stream) {
+hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l) {
   const bool vec8 =
       p.head_dim % 8 == 0 && p.s_tok % 8 == 0 && p.s_head % 8 == 0 &&
       p.d_pos % 8 == 0 && p.d_head % 8 == 0 &&
@@ -154,22 +153,17 @@ hipError_t launch_copy_kv(const CopyKvParams &p, hipStream_t stream) {
       reinterpret_cast<uintptr_t>(p.dst) % 16 == 0;
   const uint64_t items =
       (uint64_t)p.tokens * p.heads * (vec8 ? p.head_dim / 8 : p.head_dim);
-  if (items == 0) return hipSuccess;
+  if (items == 0) return no_dispatch(l);
   const uint64_t blocks64 = (items + 255) / 256;
   const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
-  if (vec8)
-    copy_kv_kernel<8><<<blocks, 256, 0, stream>>>(p);
-  else
-    copy_kv_kernel<1><<<blocks, 256, 0, stream>>>(p);
-  return hipGetLastError();
+  if (vec8) return dispatch(copy_kv_kernel<8>, dim3(blocks), dim3(256), 0, l, p);
+  return dispatch(copy_kv_kernel<1>, dim3(blocks), dim3(256), 0, l, p);
 }
 
-hipError_t launch_qk_norm_rope(const QkNormRopeParams &p,
-                               hipStream_t stream) {
+hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
   const uint32_t groups = p.tokens * (p.q_heads + p.kv_heads);
-  if (groups == 0) return hipSuccess;
-  qk_norm_rope_kernel<<<groups, 64, 0, stream>>>(p);
-  return hipGetLastError();
+  if (groups == 0) return no_dispatch(l);
+  return dispatch(qk_norm_rope_kernel, dim3(groups), dim3(64), 0, l, p);
 }
 
 }  // namespace kernels

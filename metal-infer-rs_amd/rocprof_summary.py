@@ -1,0 +1,159 @@
+"""Summaries of rocprofv3 output for the committed profile records.
+
+  stats DIR --command CMD
+      Markdown table of a `rocprofv3 --kernel-trace --stats --output-format csv`
+      run: calls and average / min / max duration per kernel.
+  traffic --copy-bytes N --run WORKLOAD=FETCH_DIR,WRITE_DIR ... --command CMD
+      HBM bytes per dispatch of each workload's dominant kernel from two
+      `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE; KiB per
+      dispatch), each scaled by what the same counter reads for the copy
+      kernel (copy_kv_kernel, N bytes read and N written) that ran in the same
+      process. Writes a JSON record and a markdown table.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import re
+import sys
+from collections import defaultdict
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+
+# Library launch record -> rocprof kernel of each workload's dominant kernel.
+DOMINANT = {
+    "c2": ("attn_rows", "attn_rows_kernel"),
+    "c4": ("attn_rows_batched", "attn_rows_kernel"),
+    "c3": ("attn_prefill", "attn_prefill_kernel"),
+    "c5": ("attn_prefill", "attn_prefill_kernel"),
+}
+COPY_KERNEL = "copy_kv_kernel"
+
+
+def short(name: str) -> str:
+    """'void mi::kernels::(anonymous namespace)::attn_rows_kernel<128, 4, 8>(...)'
+    -> 'attn_rows_kernel<128, 4, 8>'."""
+    m = re.search(r"(\w+_kernel(?:<[^>]*>)?)\(", name)
+    return m.group(1) if m else name
+
+
+def base(name: str) -> str:
+    return short(name).split("<")[0]
+
+
+def one_file(directory: str, suffix: str) -> Path:
+    found = sorted(glob.glob(f"{directory}/**/*{suffix}", recursive=True))
+    if not found:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    return Path(found[0])
+
+
+def stats(args) -> None:
+    """Per (kernel, grid) durations from the kernel trace (one kernel serves
+    several workloads, told apart by grid), then rocprofv3's own --stats
+    table."""
+    trace: dict[tuple[str, str], list[float]] = defaultdict(list)
+    for r in csv.DictReader(one_file(args.dir, "kernel_trace.csv").open()):
+        grid = "x".join(str(int(r[f"Grid_Size_{a}"]) // int(r[f"Workgroup_Size_{a}"]))
+                        for a in "XYZ")
+        ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        trace[(short(r["Kernel_Name"]), grid)].append(ns / 1e3)
+    print(f"# Kernel durations: {args.title}\n")
+    print(f"Command (from the repository root on the GPU box):\n\n    {args.command}\n")
+    print("## Per kernel and workgroup grid (kernel trace)\n")
+    print("| kernel | workgroups | calls | average (us) | median (us) | min (us) | max (us) |")
+    print("|---|---|---:|---:|---:|---:|---:|")
+    for (name, grid), us in sorted(trace.items(), key=lambda kv: -sum(kv[1])):
+        us.sort()
+        print(f"| `{name}` | {grid} | {len(us)} | {sum(us) / len(us):.2f} | "
+              f"{us[len(us) // 2]:.2f} | {us[0]:.2f} | {us[-1]:.2f} |")
+    rows = list(csv.DictReader(one_file(args.dir, "kernel_stats.csv").open()))
+    print("\n## rocprofv3 --stats\n")
+    print("| kernel | calls | average (us) | min (us) | max (us) | share of GPU time |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+              f"{float(r['Percentage']):.1f}% |")
+
+
+def counter_means(directory: str, counter: str) -> dict[str, tuple[float, int]]:
+    """Mean value per dispatch of `counter` for every kernel base name."""
+    values: dict[str, list[float]] = defaultdict(list)
+    for r in csv.DictReader(one_file(directory, "counter_collection.csv").open()):
+        if r["Counter_Name"] == counter:
+            values[base(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in values.items()}
+
+
+def traffic(args) -> None:
+    import workloads
+
+    out = {"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, KiB per dispatch",
+           "command": args.command, "copy_bytes": args.copy_bytes, "workloads": {}}
+    lines = []
+    for spec in args.run:
+        workload, dirs = spec.split("=", 1)
+        fetch_dir, write_dir = dirs.split(",")
+        record, kernel = DOMINANT[workload]
+        fetch = counter_means(fetch_dir, "FETCH_SIZE")
+        write = counter_means(write_dir, "WRITE_SIZE")
+        copy_kib = args.copy_bytes / 1024
+        f_scale = copy_kib / fetch[COPY_KERNEL][0]
+        w_scale = copy_kib / write[COPY_KERNEL][0]
+        fetch_b = fetch[kernel][0] * f_scale * 1024
+        write_b = write[kernel][0] * w_scale * 1024
+        case = workloads.case(int(workload[1:]), generate=False)
+        algorithmic = case.algorithmic_bytes()
+        out["workloads"][workload] = {
+            "kernel": record, "rocprof_kernel": kernel,
+            "dispatches": fetch[kernel][1],
+            "fetch_kib_raw": round(fetch[kernel][0], 1), "write_kib_raw": round(write[kernel][0], 1),
+            "copy_fetch_kib_raw": round(fetch[COPY_KERNEL][0], 1),
+            "copy_write_kib_raw": round(write[COPY_KERNEL][0], 1),
+            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+            "fetch_bytes": int(fetch_b), "write_bytes": int(write_b),
+            "traffic_bytes": int(fetch_b + write_b), "algorithmic_bytes": algorithmic,
+            "traffic_over_algorithmic": round((fetch_b + write_b) / algorithmic, 3)}
+        e = out["workloads"][workload]
+        lines.append(f"| {workload} | `{kernel}` | {e['dispatches']} | {e['fetch_kib_raw']:.0f} | "
+                     f"{e['write_kib_raw']:.0f} | {e['fetch_scale']:.3f} / {e['write_scale']:.3f} | "
+                     f"{e['traffic_bytes'] / 1e6:.2f} | {algorithmic / 1e6:.2f} | "
+                     f"{e['traffic_over_algorithmic']:.2f} |")
+    Path(args.json).write_text(json.dumps(out, indent=1) + "\n")
+    with open(args.md, "w") as f:
+        f.write("# HBM traffic per dispatch (rocprofv3 PMC)\n\n")
+        f.write("Two counter passes per workload, FETCH_SIZE then WRITE_SIZE (KiB per "
+                "dispatch), each scaled by the reading of the same counter for "
+                f"copy_kv_kernel copying {args.copy_bytes} bytes (read and written once) "
+                "in the same process.\n\nCommands (from the repository root on the GPU box):\n\n")
+        for c in args.command.split(" ;; "):
+            f.write(f"    {c}\n")
+        f.write("\n| workload | kernel | dispatches | FETCH KiB raw | WRITE KiB raw | "
+                "scale fetch / write | traffic MB | algorithmic MB | ratio |\n")
+        f.write("|---|---|---:|---:|---:|---:|---:|---:|---:|\n")
+        f.write("\n".join(lines) + "\n")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    s.add_argument("--title", default="")
+    s.add_argument("--command", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("--copy-bytes", type=int, required=True)
+    t.add_argument("--run", action="append", required=True)
+    t.add_argument("--command", required=True)
+    t.add_argument("--json", required=True)
+    t.add_argument("--md", required=True)
+    args = ap.parse_args()
+    stats(args) if args.cmd == "stats" else traffic(args)
+
+
+if __name__ == "__main__":
+    main()

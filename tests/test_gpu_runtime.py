@@ -69,7 +69,9 @@ def test_kernel_profiling_records_each_launch(ctx):
         profiles = ctx.take_kernel_profiles()
     finally:
         ctx.set_kernel_profiling(False)
-    assert [name for name, _ in profiles] == ["attn_rows", "attn_naive"]
+    # The split-K decode of 1024 keys runs in several blocks, so its merge
+    # pass is a launch of its own.
+    assert [name for name, _ in profiles] == ["attn_rows", "attn_merge", "attn_naive"]
     assert all(ns > 0 for _, ns in profiles)
 
 
