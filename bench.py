@@ -318,7 +318,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the attention path has no multi-GPU "
-              "component in this build (see DESIGN.md for how it would shard)", file=sys.stderr)
+              "component in this build; a multi-GPU layout is design-only here", file=sys.stderr)
         return 2
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
     unknown = set(chosen) - {"c2", "c3", "c4", "c5"}

@@ -4,7 +4,7 @@
  * This is the drop-in boundary for metal-infer's attention hot path
  * (stratorys/metal-infer-rs; every citation below is relative to that
  * repository's root). A Rust `extern "C"` façade in a HIP backend of
- * metal-infer-core binds exactly these symbols; INTEGRATION.md shows it.
+ * metal-infer-core binds exactly these symbols.
  *
  * Conventions
  *  - Every fallible call returns an mi_status. On failure a human-readable
@@ -14,7 +14,10 @@
  *    the caller keeps the memory alive until the batch that uses it has been
  *    waited on (the same contract as ops.rs:1311-1313).
  *  - A batch is an in-order sequence of kernels on the context's HIP stream
- *    (the counterpart of one MTLCommandBuffer). Nothing runs until commit.
+ *    (the counterpart of one MTLCommandBuffer). Each operation is enqueued
+ *    on the stream when it is called, so the GPU may start before commit;
+ *    commit closes the batch and wait / finish block until it is done.
+ *    Outputs are readable only after wait.
  *  - The library owns only scratch memory (a per-batch arena) and the
  *    KV caches it creates; everything else is caller-owned.
  *  - Contexts are single-threaded, like MetalContext (`!Send + !Sync`).
@@ -203,8 +206,10 @@ void *mi_batch_stream(mi_batch *batch);
 /* ---------------------------------------------------------- profiling -- */
 
 /* set_kernel_profiling / take_kernel_profiles (context.rs:602-700): when
- * enabled, every kernel a batch launches is bracketed by HIP events on the
- * batch's stream and reported per launch after wait. */
+ * enabled, every kernel a batch launches carries start / stop HIP events
+ * bound to its dispatch (hipExtLaunchKernelGGL), and its execution time is
+ * reported per launch after wait. A split-K attention records its split
+ * pass ("attn_rows") and merge pass ("attn_merge") separately. */
 mi_status mi_context_set_kernel_profiling(mi_context *ctx, int32_t enabled);
 mi_status mi_context_take_kernel_profiles(mi_context *ctx,
                                           mi_kernel_profile *out,

@@ -7,7 +7,10 @@
  *
  * Every function restates a piece of the reference (stratorys/metal-infer-rs,
  * paths relative to the reference root) and cites the lines it follows.
- * Parity pins for each function are listed in oracle/README.md.
+ * tests/test_oracle.py pins each function against checks that share none of
+ * its code (numpy's IEEE conversions, torch float64 SDPA fixtures,
+ * transformers' Qwen3 RMSNorm/RoPE, closed forms, invariants, brute force)
+ * and plants plausible mistakes to show that the pins catch them.
  */
 #ifndef MI_ATTN_ORACLE_H
 #define MI_ATTN_ORACLE_H
