@@ -27,7 +27,7 @@ namespace {
 using namespace mi::dev;
 
 constexpr int BM = kPrefillBlockM;  // packed rows per workgroup
-constexpr int BN = 64;              // keys per KV tile
+constexpr int BN = kPrefillBlockN;  // keys per KV tile
 constexpr int THREADS = 256;        // 4 waves x 32 rows
 
 typedef __fp16 h8_t __attribute__((ext_vector_type(8)));
@@ -60,6 +60,24 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   const f2_t v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
 }
+
+// Device-scope (agent) relaxed 8-byte accesses: the stores write through to
+// the device-coherent level and the loads read from it, so split partials
+// pass between workgroups on different XCDs without a cache-wide fence.
+__device__ __forceinline__ void store_coherent2(float *ptr, float a, float b) {
+  const uint64_t bits = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(ptr), bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent2(const float *ptr) {
+  const uint64_t bits =
+      __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(ptr)),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every
+// vector-memory access of this wave, stores included, has completed.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // O and l are rescaled only when a row's max grows past its reference by
 // more than 2^8. The reference may then lag the true max, which keeps
@@ -95,18 +113,26 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   // by linear id, so id % 8 selects the XCD. When the KV heads split evenly
   // over the XCDs, each XCD gets whole heads (their K/V stay in its L2);
   // within an XCD the heaviest row tiles go first.
-  uint32_t tile, kvh;
+  // Dispatch order: workgroups are handed out in linear-id order, and
+  // round-robin over the 8 XCDs, so id % 8 selects the XCD. When the KV
+  // heads split evenly over the XCDs, each XCD gets whole heads (their K/V
+  // stay in its L2). Within a head, row tiles go heaviest first and the key
+  // splits of one row tile go together.
+  uint32_t tile, kvh, split;
   {
-    const uint32_t id = blockIdx.x + gridDim.x * blockIdx.y;
-    const uint32_t H = gridDim.y;
+    const uint32_t id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const uint32_t H = p.kv_heads, S = gridDim.z;
+    uint32_t rest;
     if (H % 8 == 0) {
       const uint32_t xcd = id % 8, k = id / 8, per = H / 8;
       kvh = xcd * per + k % per;
-      tile = p.row_tiles - 1 - k / per;
+      rest = k / per;
     } else {
-      tile = p.row_tiles - 1 - blockIdx.x;
-      kvh = blockIdx.y;
+      kvh = id % H;
+      rest = id / H;
     }
+    tile = p.row_tiles - 1 - rest / S;
+    split = rest % S;
   }
   const uint32_t row0 = tile * BM;
   const uint32_t my_row = row0 + wave * 32 + n;
@@ -119,6 +145,12 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   const uint32_t kmax =
       p.causal != 0 ? (uint32_t)min(L, off + t_last + 1) : (uint32_t)L;
   const uint32_t n_tiles = (kmax + BN - 1) / BN;
+  // This split's key tiles [t_begin, t_end) and the row tile's split count.
+  const uint32_t per_split = p.split_tiles != 0 ? p.split_tiles : n_tiles;
+  const uint32_t t_begin = split * per_split;
+  if (t_begin >= n_tiles) return;  // the row tile needs fewer splits
+  const uint32_t t_end = min(n_tiles, t_begin + per_split);
+  const bool partial_out = n_tiles > per_split;
   // Last visible key of this lane's row, and of the tile's first row (below
   // which no key needs a mask).
   const uint64_t lim =
@@ -257,7 +289,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     // visible to every row).
     if (__any((mx - m_run) * c2 > kRescaleLog2)) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = exp2_raw((m_run - m_new) * c2);
+      // A row that has seen no visible key yet (only possible in a later
+      // key split) keeps m = -inf and nothing to rescale.
+      const float alpha = m_new == -INFINITY ? 1.0f : exp2_raw((m_run - m_new) * c2);
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
@@ -265,7 +299,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
       m_run = m_new;
     }
-    const float mc = m_run * c2;
+    const float mc = m_run == -INFINITY ? 0.0f : m_run * c2;
     uint32_t pw[2][8];  // P as packed f16 pairs, in accumulator order
     float psum = 0.0f;
 #pragma unroll
@@ -306,25 +340,123 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     // Tile it+1 (loaded during the previous tile) goes to the other stage,
     // whose last readers finished before the previous barrier; then the
     // loads for tile it+2 are issued to overlap the next tile's compute.
-    if (it + 1 < n_tiles) store_tile((it + 1) & 1);
+    if (it + 1 < t_end) store_tile((it + 1) & 1);
     __syncthreads();
-    if (it + 2 < n_tiles) load_tile(j0 + 2 * BN);
+    if (it + 2 < t_end) load_tile(j0 + 2 * BN);
   };
 
   // Tiles wholly inside the first row's window need no mask.
-  const uint32_t n_full = (uint32_t)min((uint64_t)n_tiles, (full_lim + 1) / BN);
-  load_tile(0);
-  store_tile(0);
-  if (n_tiles > 1) load_tile(BN);
+  const uint32_t n_full = (uint32_t)min((uint64_t)t_end, (full_lim + 1) / BN);
+  load_tile(t_begin * BN);
+  store_tile(t_begin & 1);
+  if (t_begin + 1 < t_end) load_tile((t_begin + 1) * BN);
   __syncthreads();
-  uint32_t it = 0;
+  uint32_t it = t_begin;
   for (; it < n_full; ++it) step(it, std::false_type{});
-  for (; it < n_tiles; ++it) step(it, std::true_type{});
+  for (; it < t_end; ++it) step(it, std::true_type{});
+
+  const float l_total = l_run + __shfl_xor(l_run, 32, 64);
+  if (partial_out) {
+    // Publish this split's unnormalised rows with device-scope stores, wait
+    // until they have completed, then count the arrival. The last split of
+    // the row tile merges; the others are done. Layout per wave, in the
+    // accumulator's own order so every store and load moves 512 contiguous
+    // bytes: float2 slot 0 = (m, l), slot 1 + 8dt + 2q + e = O values
+    // (4q + 2e, 4q + 2e + 1) of d tile dt, each slot 64 lanes wide.
+    constexpr uint32_t SLOTS = kPrefillPartialSlots(D);
+    const size_t split_stride = (size_t)p.row_tiles * p.kv_heads * 4 * SLOTS * 64 * 2;
+    float *wave_base =
+        p.partial + ((((size_t)tile * p.kv_heads + kvh) * 4 + wave) * SLOTS * 64 + lane) * 2;
+    {
+      float *mine = wave_base + split * split_stride;
+      store_coherent2(mine, m_run, l_total);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            store_coherent2(mine + (1 + 8 * dt + 2 * q + e) * 128, o[dt][4 * q + 2 * e],
+                            o[dt][4 * q + 2 * e + 1]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __shared__ uint32_t s_last;
+    __syncthreads();
+    const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
+    if (tid == 0) {
+      uint32_t *counter = p.counters + tile * p.kv_heads + kvh;
+      const uint32_t arrived =
+          __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = arrived == nsplit - 1;
+      if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last == 0 || !row_ok) return;
+    // Log-sum-exp merge in split order (deterministic whichever split
+    // arrives last); this split's own rows come from registers. Split 0
+    // holds key 0, so M is finite; a split in which a row saw no key has
+    // m = -inf and weight 0.
+    const float c2 = p.scale_log2;
+    float ms[kMaxPrefillSplits], ls[kMaxPrefillSplits];
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < (int)kMaxPrefillSplits; ++s) {
+      if (s >= (int)nsplit) break;
+      float2 ml = make_float2(m_run, l_total);
+      if (s != (int)split) ml = load_coherent2(wave_base + s * split_stride);
+      ms[s] = ml.x;
+      ls[s] = ml.y;
+      M = fmaxf(M, ml.x);
+    }
+    float lsum = 0.0f;
+    float16_t acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < (int)kMaxPrefillSplits; ++s) {
+      if (s >= (int)nsplit) break;
+      const float w = exp2_raw((ms[s] - M) * c2);
+      lsum = fmaf(ls[s], w, lsum);
+      if (s == (int)split) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(o[dt][r], w, acc[dt][r]);
+      } else {
+        const float *src = wave_base + s * split_stride;
+        float2 part[DT][8];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            part[dt][2 * q] = load_coherent2(src + (1 + 8 * dt + 2 * q) * 128);
+            part[dt][2 * q + 1] = load_coherent2(src + (2 + 8 * dt + 2 * q) * 128);
+          }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[dt][4 * q] = fmaf(part[dt][2 * q].x, w, acc[dt][4 * q]);
+            acc[dt][4 * q + 1] = fmaf(part[dt][2 * q].y, w, acc[dt][4 * q + 1]);
+            acc[dt][4 * q + 2] = fmaf(part[dt][2 * q + 1].x, w, acc[dt][4 * q + 2]);
+            acc[dt][4 * q + 3] = fmaf(part[dt][2 * q + 1].y, w, acc[dt][4 * q + 3]);
+          }
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = acc[dt][r];
+    l_run = lsum;  // the normalisation below divides by the merged sum
+  } else if (!row_ok) {
+    return;
+  }
 
   // Normalise and store: lane (h, n) holds d = 32dt + 8q + 4h + 0..3.
-  const float l_total = l_run + __shfl_xor(l_run, 32, 64);
-  if (!row_ok) return;
-  const float inv = 1.0f / l_total;
+  const float inv = 1.0f / (partial_out ? l_run : l_total);
   uint16_t *orow =
       p.out + (int64_t)my_t * p.o_tok + (int64_t)(kvh * G + my_g) * p.o_head;
 #pragma unroll
@@ -345,7 +477,7 @@ bool prefill_supported(uint32_t head_dim) {
 }
 
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
-  const dim3 grid(p.row_tiles, p.kv_heads);
+  const dim3 grid(p.row_tiles, p.kv_heads, p.splits > 0 ? p.splits : 1);
   switch (head_dim) {
     case 64: return dispatch(attn_prefill_kernel<64>, grid, dim3(THREADS), 0, l, p);
     case 128: return dispatch(attn_prefill_kernel<128>, grid, dim3(THREADS), 0, l, p);

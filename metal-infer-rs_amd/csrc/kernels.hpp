@@ -118,6 +118,18 @@ struct PrefillParams {
   uint32_t tokens, q_heads, kv_heads, group, kv_length, causal, query_offset;
   uint32_t row_tiles;       // ceil(T * group / BLOCK_M)
   float scale_log2;
+  // Split-K over keys (small grids): split z of a row tile covers key tiles
+  // [z * split_tiles, (z + 1) * split_tiles); split_tiles = 0 means one split
+  // per row tile. Each split of a row tile that needs several writes its
+  // unnormalised rows (m, l, O[D]) as f32 to `partial`, laid out
+  // [splits][row_tiles][kv_heads][4 waves][kPrefillPartialSlots(D)][64 lanes]
+  // float2, then counts its arrival in counters[tile * kv_heads + kv_head];
+  // the last split to arrive merges all of them in split order and resets
+  // the counter to zero.
+  float *partial;
+  uint32_t *counters;
+  uint32_t split_tiles;
+  uint32_t splits;
 };
 
 // Split pass (one workgroup per key block; writes the output directly when a
@@ -140,10 +152,20 @@ hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l);
 hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l);
 
 // Rows of the packed (token, head-in-group) M dimension per prefill
-// workgroup.
+// workgroup, and keys per KV tile.
 constexpr uint32_t kPrefillBlockM = 128;
+constexpr uint32_t kPrefillBlockN = 64;
+// Most key splits of one prefill row tile.
+constexpr uint32_t kMaxPrefillSplits = 8;
+// float2 slots per lane of a split partial: (m, l), then O[D] in pairs
+// (each lane holds D / 2 values of its row).
+constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim / 4; }
 bool prefill_supported(uint32_t head_dim);
+// Grid (row_tiles, kv_heads, splits); one launch, split merges included.
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
+// Capacity of a context's split-K arrival counters (row tiles x KV heads of
+// a split prefill grid).
+constexpr uint32_t kSplitCounters = 4096;
 
 }  // namespace kernels
 }  // namespace mi

@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "kernels.hpp"
 #include "runtime.hpp"
@@ -98,6 +99,49 @@ mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t ma
   return MI_OK;
 }
 
+// Key splits for prefill grids too small to fill the chip (fewer than two
+// workgroups per CU): the causally heavy row tiles are cut into ranges of
+// whole key tiles, so no workgroup walks the full key range while CUs idle.
+// The split count is the largest (up to kMaxPrefillSplits) whose non-empty
+// pieces still fit on the chip at once (two workgroups per CU): beyond that
+// the pieces queue and each one's fixed cost (Q load, first K/V round trip,
+// partial write) outweighs the balance. The last split of a row tile to
+// finish merges the f32 partials. Problems with fewer than 8 key tiles are
+// not split.
+void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t query_offset) {
+  p->splits = 1;
+  p->block_keys = 0;
+  const uint64_t row_tiles = p->grid[0];
+  const uint64_t wgs = row_tiles * p->grid[1];
+  const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1);
+  const uint64_t counters = ctx ? ctx->split_counter_count : kernels::kSplitCounters;
+  if (wgs >= 2 * cus || wgs > counters) return;
+  // Key tiles of each row tile (the kernel's causal window of its last row).
+  std::vector<uint32_t> tiles(row_tiles);
+  uint32_t max_tiles = 0;
+  for (uint64_t t = 0; t < row_tiles; ++t) {
+    const uint64_t last_row = std::min<uint64_t>((uint64_t)p->T * p->G, (t + 1) * kernels::kPrefillBlockM) - 1;
+    const uint64_t t_last = last_row / p->G;
+    const uint64_t kmax = causal ? std::min<uint64_t>(p->L, (uint64_t)query_offset + t_last + 1) : p->L;
+    tiles[t] = ceil_div(kmax, kernels::kPrefillBlockN);
+    max_tiles = std::max(max_tiles, tiles[t]);
+  }
+  if (max_tiles < 8) return;
+  for (uint32_t want = kernels::kMaxPrefillSplits; want >= 2; --want) {
+    const uint32_t per_split = ceil_div(max_tiles, want);
+    const uint32_t splits = ceil_div(max_tiles, per_split);
+    uint64_t pieces = 0;
+    for (uint32_t n : tiles) pieces += ceil_div(n, per_split);
+    if (splits < 2 || pieces * p->grid[1] > 2 * cus) continue;
+    p->splits = splits;
+    p->block_keys = per_split * kernels::kPrefillBlockN;
+    p->grid[2] = splits;
+    p->scratch_bytes = (uint64_t)splits * wgs * 4 * kernels::kPrefillPartialSlots(p->D) * 64 *
+                       2 * sizeof(float);
+    return;
+  }
+}
+
 mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor *k,
                          const mi_tensor *v, const mi_attention_config *config, int32_t kind,
                          uint32_t block_keys, uint32_t threads, bool flash_explicit,
@@ -184,6 +228,7 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
     p.grid[0] = ceil_div((uint64_t)p.T * p.G, kernels::kPrefillBlockM);
     p.grid[1] = p.Hkv;
     p.grid[2] = 1;
+    plan_prefill_splits(ctx, &p, config->causal != 0, config->query_offset);
     *plan = p;
     return MI_OK;
   }
@@ -200,8 +245,8 @@ void fill_info(const AttnPlan &p, mi_attention_plan_info *info) {
   std::snprintf(info->kernel, sizeof info->kernel, "%s", p.kernel);
   for (int i = 0; i < 3; ++i) info->grid[i] = p.grid[i];
   info->block_threads = p.threads;
-  info->block_keys = p.family == Family::Rows ? p.block_keys : 0;
-  info->splits = p.family == Family::Rows ? p.splits : 1;
+  info->block_keys = p.family != Family::Naive ? p.block_keys : 0;
+  info->splits = p.family != Family::Naive ? p.splits : 1;
   info->scratch_bytes = p.scratch_bytes;
 }
 
@@ -283,8 +328,21 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     pp.kv_length = p.L, pp.causal = config->causal != 0, pp.query_offset = config->query_offset;
     pp.row_tiles = p.grid[0];
     pp.scale_log2 = scale * log2e;
-    return launch(batch, p.kernel,
-                  [&](const kernels::Launch &s) { return kernels::launch_prefill(pp, p.D, s); });
+    pp.splits = p.splits;
+    pp.split_tiles = p.splits > 1 ? p.block_keys / kernels::kPrefillBlockN : 0;
+    void *scratch = nullptr;
+    mi_status st;
+    if (p.splits > 1) {
+      if ((st = scratch_alloc(batch, p.scratch_bytes, &scratch)) != MI_OK) return st;
+    }
+    pp.partial = static_cast<float *>(scratch);
+    pp.counters = batch->ctx->split_counters;
+    st = launch(batch, p.kernel, [&](const kernels::Launch &s) {
+      return kernels::launch_prefill(pp, p.D, s);
+    });
+    // In-order execution makes the range reusable by later work of the batch.
+    if (scratch != nullptr) scratch_free(batch->ctx, scratch);
+    return st;
   }
   kernels::RowsParams rp{};
   rp.q = qd, rp.q_seq = 0, rp.q_tok = q->stride[0], rp.q_head = q->stride[1];

@@ -234,6 +234,17 @@ mi_status mi_context_create(int32_t device, mi_context **out) {
   // Default priority only: streams of other priorities are not used.
   err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (err != hipSuccess) return hip_fail(MI_ERR_RESOURCE, "command stream", err);
+  const uint32_t counters = kernels::kSplitCounters;
+  err = hipMalloc(&ctx->split_counters, counters * sizeof(uint32_t));
+  if (err == hipSuccess) err = hipMemset(ctx->split_counters, 0, counters * sizeof(uint32_t));
+  if (err == hipSuccess) err = hipDeviceSynchronize();
+  if (err != hipSuccess) {
+    if (ctx->split_counters != nullptr) hipFree(ctx->split_counters);
+    hipStreamDestroy(ctx->stream);
+    return hip_fail(MI_ERR_RESOURCE, "split counters", err);
+  }
+  ctx->split_counter_count = counters;
+  ctx->allocated += counters * sizeof(uint32_t);
   *out = ctx.release();
   return MI_OK;
 }
@@ -250,6 +261,7 @@ void mi_context_destroy(mi_context *ctx) {
     cache->base = nullptr;
     cache->ctx = nullptr;
   }
+  hipFree(ctx->split_counters);
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }

@@ -77,6 +77,10 @@ struct Context {
   bool profiling = false;
   std::vector<mi_kernel_profile> profiles;
   std::vector<FlashDecodeEntry> flash_decode;  // tuned table, sorted
+  // Arrival counters of split-K prefill (one per row tile and KV head). Zero
+  // between kernels: the last split to arrive resets its counter.
+  uint32_t *split_counters = nullptr;
+  uint32_t split_counter_count = 0;
 
   // Live KV caches; destroying the context releases their storage and
   // detaches them, so a cache destroyed later only frees its handle.

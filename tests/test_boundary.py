@@ -227,3 +227,40 @@ def test_flash_prefill_routes_to_mfma_kernel():
     # c3: 2048 x 2 = 4096 packed rows -> 32 row tiles per KV head
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     assert plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)["grid"][:2] == (32, 8)
+
+
+def _pieces(T, G, L, off, per_split_keys):
+    """Non-empty (row tile, key split) pieces of one KV head."""
+    tiles = []
+    for t in range(-(-T * G // 128)):
+        t_last = (min(T * G, (t + 1) * 128) - 1) // G
+        tiles.append(-(-min(L, off + t_last + 1) // 64))
+    per = per_split_keys // 64
+    return sum(-(-n // per) for n in tiles), max(tiles)
+
+
+def test_small_prefill_grids_split_the_keys():
+    # c3: 256 workgroups on 256 CUs. The split count is the largest whose
+    # non-empty pieces all fit at two workgroups per CU: 3 splits of 11 key tiles.
+    q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
+    p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
+    assert p["grid"] == (32, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
+    # (m, l) + 128 O values per row as f32, for 128 rows per row tile
+    assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 4) * 64 * 2 * 4
+    pieces, max_tiles = _pieces(2048, 2, 2048, 0, p["block_keys"])
+    assert pieces * 8 <= 2 * 256
+    finer = -(-max_tiles // 4) * 64  # one more split would not fit
+    assert _pieces(2048, 2, 2048, 0, finer)[0] * 8 > 2 * 256
+    # c5 fills the chip on its own: no split, no scratch
+    q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
+    p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
+    assert p["splits"] == 1 and p["scratch_bytes"] == 0
+    # fewer than 8 key tiles: not split
+    q, k = tensor((128, 16, 128)), tensor((128, 8, 128))
+    assert plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)["splits"] == 1
+    # every split is a whole number of 64-key tiles, together covering the window
+    q, k = tensor((1024, 16, 128)), tensor((1024, 8, 128))
+    p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
+    assert 2 <= p["splits"] <= 8 and p["block_keys"] % 64 == 0
+    assert p["splits"] * p["block_keys"] >= 1024 > (p["splits"] - 1) * p["block_keys"]
+    assert _pieces(1024, 2, 1024, 0, p["block_keys"])[0] * 8 <= 2 * 256

@@ -130,6 +130,28 @@ def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
         assert_parity(out, ref, label=f"T={T} off={off} causal={causal}")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv,T,off,causal", [
+    (8, 8, 700, 37, True), (16, 8, 1000, 300, True), (64, 8, 520, 37, True),
+    (16, 1, 333, 300, True), (8, 2, 1500, 0, True), (8, 8, 520, 0, False)])
+def test_flash_prefill_key_splits(ctx, d, hq, hkv, T, off, causal):
+    """Small grids run heavy row tiles in several key splits plus a merge
+    pass. These geometries include row tiles whose last split starts past
+    the causal limit of their first rows (such rows see no key there)."""
+    rng = np.random.default_rng(T * 7 + hq + d)
+    L = off + T if causal else T + 40
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+    info = ctx.plan(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v),
+                    mi_attn.AttentionConfig(hq, hkv, d, causal, off), mi_attn.FLASH_PREFILL)
+    assert info["kernel"] == "attn_prefill" and info["splits"] > 1, info
+    out = run_attention(ctx, q, k, v, kind="flash-prefill", causal=causal, **geo)
+    ref = oracle_attention(q, k, v, causal=causal, **geo)
+    assert_parity(out, ref, label=f"splits={info['splits']} T={T} off={off}")
+
+
 def test_c4_batched_decode_seeded(ctx):
     """B=32 sequences, lengths ~ U[1024, 8192], one launch over all of them."""
     c = workloads.case(4)
