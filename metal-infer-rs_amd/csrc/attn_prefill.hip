@@ -75,6 +75,19 @@ __device__ __forceinline__ float2 load_coherent2(const float *ptr) {
                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
 }
+// gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
+// at lds + 16 L (lds is wave-uniform).
+__device__ __forceinline__ void load_lds16(const uint16_t *global, uint16_t *lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
+}
+// gfx950 ds_read_b64_tr_b16: 4 halves, transposed across each 16-lane group.
+__device__ __forceinline__ uint2 read_tr16(const uint16_t *lds) {
+  typedef short v4s_t __attribute__((ext_vector_type(4)));
+  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (v4s_t __attribute__((address_space(3))) *)(lds));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every
 // vector-memory access of this wave, stores included, has completed.
 constexpr int kWaitVmcnt0 = 0x0F70;
@@ -102,8 +115,22 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   constexpr int V_PER = (V_JOBS + THREADS - 1) / THREADS;
   // Two LDS stages: tile i is read from one while tile i+1 is written into
   // the other, so one barrier per tile suffices.
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds2[2][BN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds2[2][D * VS];
+  // D = 128: K and V tiles arrive by direct global->LDS loads as 256-byte
+  // rows with XOR-swizzled 16-byte chunks (K: chunk ^ (key & 15), V:
+  // chunk ^ 4 (key & 3)), which keeps the K operand reads and the V^T
+  // transpose reads free of bank conflicts. Other D: register staging, K
+  // padded, V stored transposed.
+  constexpr bool DIRECT = D == 128;
+  constexpr int K_ELEMS = DIRECT ? BN * D : BN * KS;
+  constexpr int V_ELEMS = DIRECT ? BN * D : D * VS;
+  // One array per stage (and the stage a compile-time choice in the loop),
+  // so alias analysis can tell the direct loads into one stage from the
+  // reads of the other and no wait for in-flight loads is inserted before
+  // every LDS read.
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds_a[K_ELEMS], k_lds_b[K_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds_a[V_ELEMS], v_lds_b[V_ELEMS];
+  auto k_stage = [&](int st) __attribute__((always_inline)) -> uint16_t * { return st ? k_lds_b : k_lds_a; };
+  auto v_stage = [&](int st) __attribute__((always_inline)) -> uint16_t * { return st ? v_lds_b : v_lds_a; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -196,8 +223,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     }
   };
   auto store_tile = [&](int stage) {
-    uint16_t *k_lds = k_lds2[stage];
-    uint16_t *v_lds = v_lds2[stage];
+    uint16_t *k_lds = k_stage(stage);
+    uint16_t *v_lds = v_stage(stage);
 #pragma unroll
     for (int i = 0; i < K_CHUNKS; ++i) {
       const int c = tid + i * THREADS;
@@ -235,11 +262,42 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   float l_run = 0.0f;       // this half-wave's share of the row sum
   const float c2 = p.scale_log2;
 
-  auto step = [&](uint32_t it, auto mask_tag) {
+  // Direct loads of tile `ti` into LDS stage `stage`: each wave fills four
+  // 1 KB blocks, lane L writing bytes 16L..16L+15 of a block, so the lane
+  // fetches the global 16 bytes that belong at that swizzled position.
+  auto issue_tile = [&](uint32_t ti, int stage) {
+    const uint32_t j0 = ti * BN;
+    const uint16_t *kt = kbase + (int64_t)j0 * p.k_pos;
+    const uint16_t *vt = vbase + (int64_t)j0 * p.v_pos;
+    const int last = j0 + BN > kmax ? (int)(kmax - 1 - j0) : BN - 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = wave * 4 + i;
+      const int row = blk * 4 + (lane >> 4);
+      const int pc = lane & 15;
+      const int rr = min(row, last);
+      load_lds16(kt + (uint32_t)(rr * p.k_pos + ((pc ^ (row & 15)) * 8)),
+                 k_stage(stage) + blk * 512);
+      load_lds16(vt + (uint32_t)(rr * p.v_pos + ((pc ^ ((row & 3) << 2)) * 8)),
+                 v_stage(stage) + blk * 512);
+    }
+  };
+  // Lane roles in the V^T transpose reads (ds_read_b64_tr_b16): within each
+  // 16-lane group g, output lane 4a + b, element j receives element b of the
+  // 8 bytes addressed by lane a + 4j. Lane (a4, jj) of group g therefore
+  // addresses key 4 (g / 2) + jj (+ 8 for the second read) at d offset
+  // 16 (g % 2) + 4 a4, so output lane (h, n) gets 4 keys of column n.
+  const int tr_g = lane >> 4, tr_a = lane & 3, tr_j = (lane >> 2) & 3;
+  const int tr_key = 4 * (tr_g >> 1) + tr_j;
+  const int tr_off = tr_key * D + 4 * (tr_a & 1);
+  const int tr_chunk = 2 * (tr_g & 1) + (tr_a >> 1);
+
+  auto step = [&](uint32_t it, auto mask_tag, auto stage_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int ST = decltype(stage_tag)::value;  // LDS stage of tile it
     const uint32_t j0 = it * BN;
-    const uint16_t *k_lds = k_lds2[it & 1];
-    const uint16_t *v_lds = v_lds2[it & 1];
+    const uint16_t *k_lds = ST ? k_lds_b : k_lds_a;
+    const uint16_t *v_lds = ST ? v_lds_b : v_lds_a;
 
     // S^T[key][row] for the 64 keys of the tile: two 32-key M tiles. MFMA
     // phases run at raised wave priority, so while one wave of a SIMD feeds
@@ -252,8 +310,12 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
       for (int r = 0; r < 16; ++r) s[mt][r] = 0.0f;
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        const h8_t a = as_h8(*reinterpret_cast<const uint4 *>(
-            k_lds + (32 * mt + n) * KS + 16 * c + 8 * h));
+        const uint16_t *kp;
+        if constexpr (DIRECT)
+          kp = k_lds + (32 * mt + n) * D + (((2 * c + h) ^ (n & 15)) * 8);
+        else
+          kp = k_lds + (32 * mt + n) * KS + 16 * c + 8 * h;
+        const h8_t a = as_h8(*reinterpret_cast<const uint4 *>(kp));
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[c], s[mt], 0, 0, 0);
       }
     }
@@ -324,36 +386,78 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
                                       pw[mt][base + 2], pw[mt][base + 3]));
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const h8_t a = as_h8(*reinterpret_cast<const uint4 *>(
-            v_lds + (32 * dt + n) * VS + 16 * c + 8 * h));
+        h8_t a;
+        if constexpr (DIRECT) {
+          const int sw = ((4 * dt + tr_chunk) ^ (tr_j << 2)) * 8;
+          const uint16_t *v0 = v_lds + 16 * c * D + tr_off + sw;
+          const uint2 l2 = read_tr16(v0), h2 = read_tr16(v0 + 8 * D);
+          a = as_h8(make_uint4(l2.x, l2.y, h2.x, h2.y));
+        } else {
+          a = as_h8(*reinterpret_cast<const uint4 *>(v_lds + (32 * dt + n) * VS + 16 * c + 8 * h));
+        }
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[dt], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadAhead, 1);
+    constexpr int PV_READS = DIRECT ? 2 : 1;  // LDS reads per PV MFMA
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, PV_READS * kReadAhead, 1);
 #pragma unroll
     for (int k = 0; k < 4 * DT - kReadAhead; ++k) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, PV_READS, 1);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 1);
     __builtin_amdgcn_s_setprio(0);
     // Tile it+1 (loaded during the previous tile) goes to the other stage,
     // whose last readers finished before the previous barrier; then the
     // loads for tile it+2 are issued to overlap the next tile's compute.
-    if (it + 1 < t_end) store_tile((it + 1) & 1);
-    __syncthreads();
-    if (it + 2 < t_end) load_tile(j0 + 2 * BN);
+    if constexpr (DIRECT) {
+      // Tile it+1 (issued a tile ago) has landed in every wave's part of
+      // the other stage; after the barrier nobody reads this stage, which
+      // then receives tile it+2.
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (it + 2 < t_end) issue_tile(it + 2, ST);
+    } else {
+      if (it + 1 < t_end) store_tile(ST ^ 1);
+      __syncthreads();
+      if (it + 2 < t_end) load_tile(j0 + 2 * BN);
+    }
   };
 
   // Tiles wholly inside the first row's window need no mask.
   const uint32_t n_full = (uint32_t)min((uint64_t)t_end, (full_lim + 1) / BN);
-  load_tile(t_begin * BN);
-  store_tile(t_begin & 1);
-  if (t_begin + 1 < t_end) load_tile((t_begin + 1) * BN);
+  // Tile t_begin + k lives in stage k & 1.
+  if constexpr (DIRECT) {
+    issue_tile(t_begin, 0);
+    if (t_begin + 1 < t_end) issue_tile(t_begin + 1, 1);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  } else {
+    load_tile(t_begin * BN);
+    store_tile(0);
+    if (t_begin + 1 < t_end) load_tile((t_begin + 1) * BN);
+  }
   __syncthreads();
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   uint32_t it = t_begin;
-  for (; it < n_full; ++it) step(it, std::false_type{});
-  for (; it < t_end; ++it) step(it, std::true_type{});
+  for (; it + 1 < n_full; it += 2) {
+    step(it, std::false_type{}, S0{});
+    step(it + 1, std::false_type{}, S1{});
+  }
+  if (it < n_full) {
+    step(it, std::false_type{}, S0{});
+    ++it;
+  }
+  // The masked tail continues the stage alternation.
+  if (((it - t_begin) & 1) != 0 && it < t_end) {
+    step(it, std::true_type{}, S1{});
+    ++it;
+  }
+  for (; it + 1 < t_end; it += 2) {
+    step(it, std::true_type{}, S0{});
+    step(it + 1, std::true_type{}, S1{});
+  }
+  if (it < t_end) step(it, std::true_type{}, S0{});
 
   const float l_total = l_run + __shfl_xor(l_run, 32, 64);
   if (partial_out) {
