@@ -146,8 +146,9 @@ def timed(ctx, hip, enqueue, steps: int, eager: bool, reps: int) -> tuple[int, f
 
 def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, float, dict]:
     """The dominant kernel (largest total time) of `count` eager calls, its
-    average duration per launch (s), and every kernel's average, from HIP
-    events placed around each launch on the batch's stream."""
+    median duration per launch (s), and every kernel's median, from the
+    start / stop events the library binds to each dispatch on the batch's
+    stream (hipExtLaunchKernelGGL)."""
     ctx.take_kernel_profiles()
     ctx.set_kernel_profiling(True)
     try:
@@ -162,9 +163,11 @@ def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, floa
     by_name: dict[str, list[float]] = {}
     for name, ns in profiles:
         by_name.setdefault(name, []).append(ns)
-    average = {n: sum(v) / len(v) * 1e-9 for n, v in by_name.items()}
+    # Median per kernel: a few launches that wait on the host or on a clock
+    # change would otherwise skew a µs-scale kernel's mean.
+    typical = {n: float(np.median(v)) * 1e-9 for n, v in by_name.items()}
     name = max(by_name, key=lambda n: sum(by_name[n]))
-    return name, average[name], average
+    return name, typical[name], typical
 
 
 def measured_traffic(workload: str, kernel: str):
