@@ -215,6 +215,56 @@ def bench_decode(ctx, hip, steps, warmup, eager):
                    kernels=kernels, bytes=nbytes)
 
 
+def bench_decode_step(ctx, hip, steps):
+    """One c2-sized decode step in qwen3.rs:704-750 order (Q/K norm + RoPE with
+    K into the cache, V append, FlashDecode over the prefix: four kernels),
+    replayed from a graph captured with the library's capture API, against
+    the same step enqueued eagerly. Seconds per step for each."""
+    c = workloads.case(2)
+    hq, hkv, d, L = c.q_heads, c.kv_heads, c.head_dim, c.kv_length
+    pos = L - 1
+    cache = ctx.kv_cache(1, hkv, d, L)
+    key, value = cache.layer(0)
+    ctx.upload(key, c.k)
+    ctx.upload(value, c.v)
+    weights = ctx.tensor(np.full(d, np.float16(1.0).view(np.uint16), dtype=np.uint16))
+    q_in = ctx.tensor(c.q)
+    k_in = ctx.tensor(c.k[pos:pos + 1].copy())
+    v_in = ctx.tensor(c.v[pos:pos + 1].copy())
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
+    rope = mi_attn.QkNormRopeCacheConfig(pos, 1_000_000.0, 1e-6)
+    out = ctx.empty(c.q.shape)
+
+    def enqueue(batch, i):
+        q_rot = batch.qk_norm_rope_cache(q_in, k_in, weights, weights, key, rope)
+        batch.copy_into_cache(v_in, value, pos)
+        return batch.attention(q_rot, key.prefix(L), value.prefix(L), cfg, mi_attn.FLASH_DECODE,
+                               out=out)
+
+    eager = time_eager(ctx, hip, enqueue, steps)
+    capture = ctx.begin_capture()
+    enqueue(capture, 0)
+    graph = capture.end_capture()
+    graph.launch()
+    ctx.synchronize()
+    start, end = hip.event(), hip.event()
+    batch = ctx.begin_batch()  # only for the stream handle; the replays run on it
+    stream = ctypes.c_void_p(batch.stream)
+    hip.check(hip.lib.hipEventRecord(start, stream), "record")
+    for _ in range(steps):
+        graph.launch()
+    hip.check(hip.lib.hipEventRecord(end, stream), "record")
+    hip.check(hip.lib.hipEventSynchronize(end), "sync")
+    batch.finish()
+    ms = ctypes.c_float()
+    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, end), "elapsed")
+    graph.destroy()
+    cache.close()
+    return {"workload": "c2 decode step: qk_norm_rope_cache + copy_into_cache + FlashDecode "
+                        "(4 kernels), same cache slot every step",
+            "graph_us": round(ms.value * 1e3 / steps, 3), "eager_us": round(eager * 1e6, 3)}
+
+
 def bench_batched_decode(ctx, hip, steps, eager):
     c = workloads.case(4)
     B, hq, hkv, d, cap = c.batch, c.q_heads, c.kv_heads, c.head_dim, c.kv_length
@@ -354,6 +404,10 @@ def main() -> int:
             "roofline": roof})
     else:
         log("c2 not selected: the headline fields stay null (profiling run)")
+    if "c2" in chosen and not args.eager:
+        result["decode_step"] = bench_decode_step(ctx, hip, 256)
+        log(f"decode step: graph {result['decode_step']['graph_us']} us, "
+            f"eager {result['decode_step']['eager_us']} us")
     if "c4" in chosen:
         bc, bat = bench_batched_decode(ctx, hip, 20, args.eager)
         bval = bat["bytes"] / bat["seconds"] / 1e9

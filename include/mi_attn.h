@@ -120,6 +120,7 @@ typedef struct mi_attention_plan_info {
 typedef struct mi_context mi_context;
 typedef struct mi_batch mi_batch;
 typedef struct mi_kv_cache mi_kv_cache;
+typedef struct mi_graph mi_graph;
 
 /* ------------------------------------------------------------ library -- */
 
@@ -198,10 +199,34 @@ mi_status mi_batch_wait(mi_batch *batch, mi_dispatch_stats *stats);
 mi_status mi_batch_finish(mi_batch *batch, mi_dispatch_stats *stats);
 /* Drop for an uncommitted CommandBatch (context.rs:1119-1128): nothing it
  * encoded runs... except work already handed to the stream, which is
- * drained before the arena is released. Frees `batch`. */
+ * drained before the arena is released. A capturing batch's recording is
+ * discarded. Frees `batch`. */
 void mi_batch_abandon(mi_batch *batch);
 /* The hipStream_t the batch launches on (for interop and timing). */
 void *mi_batch_stream(mi_batch *batch);
+
+/* ------------------------------------------------------------- graphs -- */
+
+/* Captured decode steps. The reference re-encodes a Metal command buffer for
+ * every token (crates/metal-infer-models/src/qwen3.rs:475-555); on MI355X a
+ * step's few small kernels are launch-bound, so a caller may record them
+ * once and replay them. mi_batch_begin_capture opens a batch whose kernels
+ * are recorded into a HIP graph (stream capture, relaxed mode) instead of
+ * running. Only enqueueing calls belong in it (attention, copy_into_cache,
+ * qk_norm_rope_cache, mi_batch_empty); no upload, download or wait.
+ * mi_batch_end_capture consumes the batch and returns the graph, which keeps
+ * the batch's scratch arena (so tensors leased during capture stay valid and
+ * every replay writes the same addresses). Each replay reads and writes the
+ * tensors, offsets and cache slots that were current at capture. */
+mi_status mi_batch_begin_capture(mi_context *ctx, mi_batch **out);
+mi_status mi_batch_end_capture(mi_batch *batch, mi_graph **out);
+/* Enqueues one replay on the context's stream (in order with batches). */
+mi_status mi_graph_launch(mi_context *ctx, mi_graph *graph);
+/* Waits for the stream, then frees the graph and releases its arena. */
+void mi_graph_destroy(mi_graph *graph);
+/* Blocks until everything enqueued on the context's stream has finished;
+ * a GPU error is MI_ERR_COMMAND. */
+mi_status mi_context_synchronize(mi_context *ctx);
 
 /* ---------------------------------------------------------- profiling -- */
 

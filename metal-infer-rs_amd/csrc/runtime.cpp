@@ -249,6 +249,8 @@ mi_status mi_context_create(int32_t device, mi_context **out) {
   return MI_OK;
 }
 
+static void release_graph(mi_graph *graph);
+
 void mi_context_destroy(mi_context *ctx) {
   if (ctx == nullptr) return;
   hipSetDevice(ctx->device);
@@ -256,6 +258,10 @@ void mi_context_destroy(mi_context *ctx) {
   for (auto &pool : ctx->pools)
     for (auto &chunk : pool->chunks) hipFree(chunk.base);
   for (auto &entry : ctx->tensors) hipFree(reinterpret_cast<void *>(entry.first));
+  for (mi_graph *graph : ctx->graphs) {
+    release_graph(graph);
+    graph->ctx = nullptr;
+  }
   for (mi_kv_cache *cache : ctx->caches) {
     hipFree(cache->base);
     cache->base = nullptr;
@@ -450,6 +456,8 @@ mi_status mi_scratch_release(mi_context *ctx, const mi_tensor *tensor) {
 mi_status mi_batch_commit(mi_batch *batch) {
   if (batch == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null batch");
   if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  if (batch->capturing)
+    return fail(MI_ERR_RESOURCE, "a capturing batch ends with mi_batch_end_capture");
   hipError_t err = hipEventRecord(batch->end, batch->ctx->stream);
   if (err != hipSuccess) return hip_fail(MI_ERR_COMMAND, "commit", err);
   batch->committed = true;
@@ -457,14 +465,14 @@ mi_status mi_batch_commit(mi_batch *batch) {
   return MI_OK;
 }
 
-static void release_batch(mi_batch *batch) {
+static void release_batch(mi_batch *batch, bool keep_pool = false) {
   for (auto &rec : batch->launches) {
     hipEventDestroy(rec.start);
     hipEventDestroy(rec.end);
   }
   if (batch->start) hipEventDestroy(batch->start);
   if (batch->end) hipEventDestroy(batch->end);
-  batch->pool->busy = false;
+  if (!keep_pool) batch->pool->busy = false;
   delete batch;
 }
 
@@ -515,10 +523,93 @@ mi_status mi_batch_finish(mi_batch *batch, mi_dispatch_stats *stats) {
 
 void mi_batch_abandon(mi_batch *batch) {
   if (batch == nullptr) return;
+  if (batch->capturing) {
+    // Close the capture and drop what it recorded.
+    hipGraph_t graph = nullptr;
+    if (hipStreamEndCapture(batch->ctx->stream, &graph) == hipSuccess && graph != nullptr)
+      hipGraphDestroy(graph);
+    (void)hipGetLastError();
+  }
   // Kernels already handed to the stream must drain before the arena they
   // use can be claimed by another batch.
   hipStreamSynchronize(batch->ctx->stream);
   release_batch(batch);
+}
+
+mi_status mi_batch_begin_capture(mi_context *ctx, mi_batch **out) {
+  mi_status st = mi_batch_begin(ctx, out);
+  if (st != MI_OK) return st;
+  mi_batch *batch = *out;
+  // The batch's own timing events are not part of the graph.
+  hipEventDestroy(batch->start);
+  hipEventDestroy(batch->end);
+  batch->start = batch->end = nullptr;
+  hipError_t err = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+  if (err != hipSuccess) {
+    release_batch(batch);
+    *out = nullptr;
+    return hip_fail(MI_ERR_COMMAND, "hipStreamBeginCapture", err);
+  }
+  batch->capturing = true;
+  return MI_OK;
+}
+
+mi_status mi_batch_end_capture(mi_batch *batch, mi_graph **out) {
+  if (batch == nullptr || out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch or output");
+  *out = nullptr;
+  if (!batch->capturing) return fail(MI_ERR_RESOURCE, "batch is not capturing");
+  Context *ctx = batch->ctx;
+  auto graph = std::make_unique<mi_graph>();
+  hipError_t err = hipStreamEndCapture(ctx->stream, &graph->graph);
+  batch->capturing = false;
+  if (err == hipSuccess)
+    err = hipGraphInstantiate(&graph->exec, graph->graph, nullptr, nullptr, 0);
+  if (err != hipSuccess) {
+    if (graph->graph != nullptr) hipGraphDestroy(graph->graph);
+    release_batch(batch);
+    return hip_fail(MI_ERR_COMMAND, "graph capture", err);
+  }
+  graph->ctx = ctx;
+  graph->pool = batch->pool;  // stays busy: replays write into its ranges
+  release_batch(batch, /*keep_pool=*/true);
+  ctx->graphs.insert(graph.get());
+  *out = graph.release();
+  return MI_OK;
+}
+
+mi_status mi_graph_launch(mi_context *ctx, mi_graph *graph) {
+  if (ctx == nullptr || graph == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null context or graph");
+  if (graph->ctx != ctx) return fail(MI_ERR_INVALID_ARGUMENT, "graph belongs to another context");
+  hipError_t err = hipGraphLaunch(graph->exec, ctx->stream);
+  if (err != hipSuccess) return hip_fail(MI_ERR_COMMAND, "hipGraphLaunch", err);
+  return MI_OK;
+}
+
+static void release_graph(mi_graph *graph) {
+  if (graph->exec != nullptr) hipGraphExecDestroy(graph->exec);
+  if (graph->graph != nullptr) hipGraphDestroy(graph->graph);
+  graph->exec = nullptr;
+  graph->graph = nullptr;
+}
+
+void mi_graph_destroy(mi_graph *graph) {
+  if (graph == nullptr) return;
+  if (graph->ctx != nullptr) {
+    hipStreamSynchronize(graph->ctx->stream);  // no replay may still use the arena
+    release_graph(graph);
+    graph->pool->busy = false;
+    graph->ctx->graphs.erase(graph);
+  }
+  delete graph;
+}
+
+mi_status mi_context_synchronize(mi_context *ctx) {
+  if (ctx == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null context");
+  hipError_t err = hipStreamSynchronize(ctx->stream);
+  if (err != hipSuccess) return hip_fail(MI_ERR_COMMAND, "GPU command failed", err);
+  return MI_OK;
 }
 
 void *mi_batch_stream(mi_batch *batch) {

@@ -85,6 +85,8 @@ struct Context {
   // Live KV caches; destroying the context releases their storage and
   // detaches them, so a cache destroyed later only frees its handle.
   std::unordered_set<mi_kv_cache *> caches;
+  // Live captured graphs (same ownership rule as caches).
+  std::unordered_set<mi_graph *> graphs;
 };
 
 struct LaunchRecord {
@@ -99,6 +101,7 @@ struct Batch {
   hipEvent_t start = nullptr;
   hipEvent_t end = nullptr;
   bool committed = false;
+  bool capturing = false;  // kernels are recorded into a HIP graph
   std::chrono::steady_clock::time_point commit_time;
   std::vector<LaunchRecord> launches;
 };
@@ -115,7 +118,7 @@ template <typename Fn>
 mi_status launch(Batch *batch, const char *kernel, Fn &&fn) {
   kernels::Launch l;
   l.stream = batch->ctx->stream;
-  if (batch->ctx->profiling) {
+  if (batch->ctx->profiling && !batch->capturing) {
     if (hipEventCreate(&l.start) != hipSuccess || hipEventCreate(&l.stop) != hipSuccess) {
       if (l.start) hipEventDestroy(l.start);
       return fail(MI_ERR_PROFILING, "could not create profiling events");
@@ -141,6 +144,12 @@ mi_status require_f16(const mi_tensor *t);
 // Opaque handle types of the C ABI.
 struct mi_context : mi::Context {};
 struct mi_batch : mi::Batch {};
+struct mi_graph {
+  mi::Context *ctx = nullptr;
+  mi::ScratchPool *pool = nullptr;  // the capturing batch's arena, kept busy
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
 struct mi_kv_cache {
   mi::Context *ctx = nullptr;
   void *base = nullptr;

@@ -114,6 +114,11 @@ def _load() -> ctypes.CDLL:
         "mi_batch_finish": (ctypes.c_int, [ctypes.c_void_p, _P(DispatchStats)]),
         "mi_batch_abandon": (None, [ctypes.c_void_p]),
         "mi_batch_stream": (ctypes.c_void_p, [ctypes.c_void_p]),
+        "mi_batch_begin_capture": (ctypes.c_int, [ctypes.c_void_p, _P(ctypes.c_void_p)]),
+        "mi_batch_end_capture": (ctypes.c_int, [ctypes.c_void_p, _P(ctypes.c_void_p)]),
+        "mi_graph_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+        "mi_graph_destroy": (None, [ctypes.c_void_p]),
+        "mi_context_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
         "mi_context_set_kernel_profiling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
         "mi_context_take_kernel_profiles": (ctypes.c_int, [ctypes.c_void_p, _P(KernelProfile),
                                                            ctypes.c_size_t, _P(ctypes.c_size_t)]),
@@ -325,6 +330,13 @@ class Context:
     def begin_batch(self) -> "Batch":
         return Batch(self)
 
+    def begin_capture(self) -> "Batch":
+        """A batch whose kernels are recorded into a graph (end_capture)."""
+        return Batch(self, capture=True)
+
+    def synchronize(self) -> None:
+        _check(lib().mi_context_synchronize(self.handle))
+
     def kv_cache(self, layers: int, kv_heads: int, head_dim: int, capacity: int) -> "KvCache":
         return KvCache(self, layers, kv_heads, head_dim, capacity)
 
@@ -397,12 +409,19 @@ def attention_kind_for_tokens(configured: int, tokens: int, active_length: int,
 class Batch:
     """CommandBatch / PendingBatch (context.rs:155-171, 1032-1083)."""
 
-    def __init__(self, ctx: Context):
+    def __init__(self, ctx: Context, capture: bool = False):
         self.ctx = ctx
         handle = ctypes.c_void_p()
-        _check(lib().mi_batch_begin(ctx.handle, ctypes.byref(handle)))
+        begin = lib().mi_batch_begin_capture if capture else lib().mi_batch_begin
+        _check(begin(ctx.handle, ctypes.byref(handle)))
         self.handle = handle
         self.stats = None
+
+    def end_capture(self) -> "Graph":
+        graph = ctypes.c_void_p()
+        handle, self.handle = self.handle, None
+        _check(lib().mi_batch_end_capture(handle, ctypes.byref(graph)))
+        return Graph(self.ctx, graph)
 
     def _out(self, shape, out: Tensor | None) -> Tensor:
         if out is not None:
@@ -491,6 +510,28 @@ class Batch:
     def __del__(self):
         try:
             self.abandon()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A captured batch (mi_batch_end_capture); launch() enqueues a replay."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self) -> None:
+        _check(lib().mi_graph_launch(self.ctx.handle, self.handle))
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", None) and self.ctx.handle:
+            lib().mi_graph_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
         except Exception:
             pass
 

@@ -108,3 +108,59 @@ def test_tuned_flash_decode_table_is_used(ctx):
     k, v = rand(8, (700, 8, 128)), rand(9, (700, 8, 128))
     out = run_attention(ctx, rng_q, k, v, kind="flash-decode", hq=16, hkv=8, d=128, off=699)
     assert out.shape == (1, 16, 128)
+
+
+# ------------------------------------------------- captured decode steps --
+
+def _decode_step(batch, q_in, k_in, v_in, weights, key, value, pos, hq, hkv, d):
+    """qwen3.rs:704-750 order: Q/K norm+RoPE (K into the cache), V append,
+    FlashDecode over the cache prefix."""
+    q_rot = batch.qk_norm_rope_cache(q_in, k_in, weights, weights, key,
+                                     mi_attn.QkNormRopeCacheConfig(pos, 1_000_000.0, 1e-6))
+    batch.copy_into_cache(v_in, value, pos)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
+    return batch.attention(q_rot, key.prefix(pos + 1), value.prefix(pos + 1), cfg,
+                           mi_attn.FLASH_DECODE)
+
+
+def test_captured_decode_step_replays_match_eager(ctx):
+    hq, hkv, d, cap, pos = 16, 8, 128, 1024, 700
+    cache = ctx.kv_cache(1, hkv, d, cap)
+    key, value = cache.layer(0)
+    batch = ctx.begin_batch()
+    batch.copy_into_cache(ctx.tensor(rand(40, (pos, hkv, d))), key, 0)
+    batch.copy_into_cache(ctx.tensor(rand(41, (pos, hkv, d))), value, 0)
+    batch.finish()
+    weights = ctx.tensor(rand(42, (d,)))
+    q_in, k_in, v_in = ctx.empty((1, hq, d)), ctx.empty((1, hkv, d)), ctx.empty((1, hkv, d))
+
+    capture = ctx.begin_capture()
+    out_graph = _decode_step(capture, q_in, k_in, v_in, weights, key, value, pos, hq, hkv, d)
+    graph = capture.end_capture()
+    other_q, other_k, other_v, other_cfg = _decode_inputs(ctx)
+    for rep in range(4):
+        ctx.upload(q_in, rand(50 + rep, (1, hq, d)))
+        ctx.upload(k_in, rand(60 + rep, (1, hkv, d)))
+        ctx.upload(v_in, rand(70 + rep, (1, hkv, d)))
+        graph.launch()
+        ctx.synchronize()
+        got = ctx.download(out_graph)
+        got_k = ctx.download(key.prefix(pos + 1))[pos]
+        # unrelated eager work between replays
+        ctx.attention(other_q, other_k, other_v, other_cfg, mi_attn.FLASH_DECODE)
+        batch = ctx.begin_batch()
+        out_eager = _decode_step(batch, q_in, k_in, v_in, weights, key, value, pos, hq, hkv, d)
+        batch.finish()
+        assert (got == ctx.download(out_eager)).all(), f"replay {rep}"
+        assert (got_k == ctx.download(key.prefix(pos + 1))[pos]).all(), f"replay {rep} cache"
+    graph.destroy()
+    cache.close()
+
+
+def test_capturing_batch_rules(ctx):
+    capture = ctx.begin_capture()
+    with pytest.raises(mi_attn.MiError, match="mi_batch_end_capture"):
+        capture.commit()
+    capture.abandon()  # drops the recording, releases the arena
+    q, k, v, cfg = _decode_inputs(ctx)
+    assert ctx.download(ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)).shape == (1, 16, 128)
