@@ -285,7 +285,11 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q,
                                       const mi_tensor *out);
 
 /* FlashDecode (block, threads) for a KV length
- * (flash_decode_configuration_for_length, context.rs:258-267). */
+ * (flash_decode_configuration_for_length, context.rs:258-267): the tuned
+ * entry, or untuned (128, 256). Untuned, mi_attention's FlashDecode runs the
+ * library default instead: 128-key splits on 512-thread workgroups with the
+ * split merge inside the launch; passing a configuration explicitly selects
+ * the reference-sized threadgroup and a separate merge launch. */
 mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx,
                                                    uint64_t length,
                                                    uint32_t *block_keys,

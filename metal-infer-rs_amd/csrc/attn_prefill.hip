@@ -61,20 +61,6 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
 }
 
-// Device-scope (agent) relaxed 8-byte accesses: the stores write through to
-// the device-coherent level and the loads read from it, so split partials
-// pass between workgroups on different XCDs without a cache-wide fence.
-__device__ __forceinline__ void store_coherent2(float *ptr, float a, float b) {
-  const uint64_t bits = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t *>(ptr), bits, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 load_coherent2(const float *ptr) {
-  const uint64_t bits =
-      __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(ptr)),
-                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
-}
 // gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
 // at lds + 16 L (lds is wave-uniform).
 __device__ __forceinline__ void load_lds16(const uint16_t *global, uint16_t *lds) {
@@ -88,9 +74,6 @@ __device__ __forceinline__ uint2 read_tr16(const uint16_t *lds) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every
-// vector-memory access of this wave, stores included, has completed.
-constexpr int kWaitVmcnt0 = 0x0F70;
 
 // O and l are rescaled only when a row's max grows past its reference by
 // more than 2^8. The reference may then lag the true max, which keeps

@@ -17,6 +17,8 @@
 //    one kernel needs an agent-scope release per workgroup, which on a
 //    multi-XCD part writes back the XCD's whole L2; measured slower than the
 //    second launch for every split size, so the kernel boundary does it.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -79,7 +81,7 @@ __device__ __forceinline__ float dot(const Vec<VEC> &a, const Vec<VEC> &b) {
 // rescale, so the cost is one memory round trip per chunk.
 constexpr int kMergeFloats = 6144;
 
-template <int D, int GC, int THREADS>
+template <int D, int GC, int THREADS, bool COHERENT = false>
 __device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
                                              uint32_t nsplits, uint16_t *out,
                                              float *buf) {
@@ -101,7 +103,12 @@ __device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
 #pragma unroll
     for (int j = 0; j < kMergeFloats / THREADS + 1; ++j) {
       const uint32_t i = tid + j * THREADS;
-      staged[j] = i < total ? src[i] : 0.0f;
+      if constexpr (COHERENT)  // written by other workgroups of this launch
+        staged[j] = i < total ? __hip_atomic_load(const_cast<float *>(src + i), __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.0f;
+      else
+        staged[j] = i < total ? src[i] : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -136,7 +143,10 @@ __device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
   }
 }
 
-template <int D, int WAVES, int GC>
+// FUSED: with more than one split, each split publishes its partial with
+// device-scope stores and counts its arrival in p.counters[unit]; the last
+// split to arrive merges all of them in split order (no second launch).
+template <int D, int WAVES, int GC, bool FUSED>
 __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     const RowsParams p) {
   constexpr int VEC = D >= 8 ? 8 : D;  // halves per lane per key row
@@ -224,20 +234,19 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
       vd[u] = load_vec<VEC>(vb + (int64_t)kk * p.v_pos);
     }
   };
-  Vec<VEC> kv[U], vv[U];
-  uint32_t key = k0 + row;
-  if (key < k1) load_batch(key, kv, vv);
-  // Every lane of a key row shares `row`, so the DPP reductions below only
-  // ever combine lanes with identical trip counts.
-  for (; key < k1; key += R * U) {
-    const uint32_t next = key + R * U;
-    Vec<VEC> kn[U], vn[U];
-    if (next < k1) load_batch(next, kn, vn);
+  // One batch of U key rows per lane: scores, online softmax, V accumulate.
+  // PARTIAL: the batch runs past the split's end, so its missing rows (which
+  // re-read row k1 - 1) get score -inf and a zero V. A batch is full or
+  // partial for a whole 16-lane key row, so every DPP reduction below only
+  // combines lanes on the same path.
+  auto consume = [&](const Vec<VEC> *kv, Vec<VEC> *vv, uint32_t key,
+                     auto partial_tag) __attribute__((always_inline)) {
+    constexpr bool PARTIAL = decltype(partial_tag)::value;
     bool valid[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      valid[u] = key + (uint32_t)(u * R) < k1;
-      if (!valid[u]) vv[u] = zero_vec<VEC>();
+      valid[u] = !PARTIAL || key + (uint32_t)(u * R) < k1;
+      if (PARTIAL && !valid[u]) vv[u] = zero_vec<VEC>();
     }
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
@@ -246,10 +255,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         s[u] = lane_group_sum<LPR>(dot<VEC>(qv[g], kv[u])) * p.scale_log2;
-        s[u] = valid[u] ? s[u] : -INFINITY;
+        if (PARTIAL) s[u] = valid[u] ? s[u] : -INFINITY;
         mx = fmaxf(mx, s[u]);
       }
-      // u = 0 is always valid here, so mx is finite.
+      // u = 0 is always valid, so mx is finite.
       const float alpha = exp2_raw(m[g] - mx);
       float pu[U];
       float ps = 0.0f;
@@ -268,10 +277,29 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
       }
       m[g] = mx;
     }
-    if (next < k1) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) kv[u] = kn[u], vv[u] = vn[u];
-    }
+  };
+  auto consume_any = [&](const Vec<VEC> *kv, Vec<VEC> *vv, uint32_t key)
+                         __attribute__((always_inline)) {
+    if (key + (uint32_t)((U - 1) * R) < k1)
+      consume(kv, vv, key, std::false_type{});
+    else
+      consume(kv, vv, key, std::true_type{});
+  };
+  // Two register buffers alternate (loop unrolled by two), so the batch in
+  // flight never has to be copied into the one being consumed.
+  Vec<VEC> ka[U], va[U], kb2[U], vb2[U];
+  uint32_t key = k0 + row;
+  if (key < k1) load_batch(key, ka, va);
+  while (key < k1) {
+    uint32_t next = key + R * U;
+    if (next < k1) load_batch(next, kb2, vb2);
+    consume_any(ka, va, key);
+    key = next;
+    if (key >= k1) break;
+    next = key + R * U;
+    if (next < k1) load_batch(next, ka, va);
+    consume_any(kb2, vb2, key);
+    key = next;
   }
 
   // Merge the key rows of this wave (lanes that differ in their row bits).
@@ -326,6 +354,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     }
     if (direct) {
       out[g * p.o_head + d] = f32_to_f16(A / L);
+    } else if constexpr (FUSED) {
+      store_coherent(part + g * (D + 2) + 2 + d, A);
+      if (d == 0) {
+        store_coherent(part + g * (D + 2), M);
+        store_coherent(part + g * (D + 2) + 1, L);
+      }
     } else {
       part[g * (D + 2) + 2 + d] = A;
       if (d == 0) {
@@ -333,6 +367,24 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         part[g * (D + 2) + 1] = L;
       }
     }
+  }
+  if constexpr (FUSED) {
+    if (direct) return;
+    // Every store of this workgroup has completed before the arrival counts.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __shared__ uint32_t s_last;
+    __shared__ float merge_buf[kMergeFloats];
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t arrived = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = arrived == nsplits - 1;
+      if (last) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last == 0) return;
+    merge_splits<D, GC, THREADS, true>(p, unit, nsplits, out, merge_buf);
   }
 }
 
@@ -370,9 +422,11 @@ hipError_t launch_rows_dwg(const RowsParams &p, RowsPhase phase, const Launch &l
   if (phase == RowsPhase::Split) {
     const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
                     p.batch * p.tokens);
-    return dispatch(attn_rows_kernel<D, WAVES, GC>, grid, dim3(WAVES * 64), 0, l, p);
+    if (p.counters != nullptr)
+      return dispatch(attn_rows_kernel<D, WAVES, GC, true>, grid, dim3(WAVES * 64), 0, l, p);
+    return dispatch(attn_rows_kernel<D, WAVES, GC, false>, grid, dim3(WAVES * 64), 0, l, p);
   }
-  if (p.max_splits <= 1) return no_dispatch(l);
+  if (p.max_splits <= 1 || p.counters != nullptr) return no_dispatch(l);
   const uint32_t units = p.batch * p.tokens * p.kv_heads * p.head_chunks;
   return dispatch(attn_merge_kernel<D, GC>, dim3(units), dim3(256), 0, l, p);
 }
@@ -392,6 +446,7 @@ hipError_t launch_rows_dw(const RowsParams &p, uint32_t chunk, RowsPhase phase,
 template <int D>
 hipError_t launch_rows_d(const RowsParams &p, uint32_t waves, uint32_t chunk,
                          RowsPhase phase, const Launch &l) {
+  if (waves == 8) return launch_rows_dw<D, 8>(p, chunk, phase, l);
   if (waves == 4) return launch_rows_dw<D, 4>(p, chunk, phase, l);
   if (waves == 2) return launch_rows_dw<D, 2>(p, chunk, phase, l);
   return hipErrorInvalidValue;

@@ -92,5 +92,27 @@ __device__ __forceinline__ float hi_f16(uint32_t packed) {
   return (float)__builtin_bit_cast(half2_t, packed).y;
 }
 
+// Device-scope (agent) relaxed accesses: stores write through to the
+// device-coherent level and loads read from it, so partial results pass
+// between workgroups on different XCDs of one launch without a cache-wide
+// fence. A writer waits for its stores (kWaitVmcnt0) before signalling.
+__device__ __forceinline__ void store_coherent(float *ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent2(float *ptr, float a, float b) {
+  const uint64_t bits = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(ptr), bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent2(const float *ptr) {
+  const uint64_t bits =
+      __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<float *>(ptr)),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): every
+// vector-memory access of this wave, stores included, has completed.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 }  // namespace dev
 }  // namespace mi

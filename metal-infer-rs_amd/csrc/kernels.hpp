@@ -51,6 +51,9 @@ struct RowsParams {
   uint16_t *out;
   int64_t o_seq, o_tok, o_head;
   float *partial;           // [units][max_splits][chunk][D + 2] f32
+  // Arrival counters, one per unit (zero between kernels), or null. Set:
+  // the last split of a unit merges (one launch). Null: the merge pass does.
+  uint32_t *counters;
   const uint32_t *lengths;  // per-sequence KV length, or null
   uint32_t batch;           // B
   uint32_t tokens;          // T
@@ -134,7 +137,9 @@ struct PrefillParams {
 
 // Split pass (one workgroup per key block; writes the output directly when a
 // row has one block) and merge pass (combines the partials of rows with more
-// than one block; no launch when max_splits <= 1). Same stream, in order.
+// than one block; no launch when max_splits <= 1 or when counters are set,
+// in which case the split pass merges). Same stream, in order. waves: 2, 4
+// or 8 per workgroup.
 enum class RowsPhase { Split, Merge };
 hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
                        uint32_t chunk, RowsPhase phase, const Launch &l);

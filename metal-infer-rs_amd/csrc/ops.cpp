@@ -22,6 +22,7 @@ struct AttnPlan {
   Family family = Family::Rows;
   uint32_t T = 0, Hq = 0, Hkv = 0, D = 0, L = 0, G = 0;
   uint32_t waves = 4, chunk = 1, block_keys = 0, splits = 1;
+  bool fused = false;            // rows: the last split merges (no merge launch)
   uint64_t units = 0;            // rows-kernel (row, KV head, chunk) units
   uint64_t scratch_bytes = 0;
   uint32_t grid[3] = {0, 0, 0};
@@ -63,32 +64,41 @@ uint32_t default_block(const Context *ctx, uint64_t units, uint32_t keys) {
 }
 
 // FlashDecode (block, threads) for a length (context.rs:258-267): the tuned
-// table if any, else (128, 256) — the reference's (64, 256) default is an
-// Apple-GPU choice; 128-key splits measured fastest here.
-void flash_config_for_length(const Context *ctx, uint64_t length, uint32_t *block,
+// table if any (returns true), else (128, 256) — the reference's (64, 256)
+// default is an Apple-GPU choice; 128-key splits measured fastest here.
+bool flash_config_for_length(const Context *ctx, uint64_t length, uint32_t *block,
                              uint32_t *threads) {
   if (ctx != nullptr)
     for (const auto &e : ctx->flash_decode)
       if (length <= e.limit) {
         *block = e.block_keys;
         *threads = e.threads;
-        return;
+        return true;
       }
   *block = 128;
   *threads = 256;
+  return false;
 }
 
+// threads = 0 picks the default: for one decode token of one sequence, 8
+// waves per workgroup and the split merge inside the launch (measured on
+// MI355X at c2: 9.2 us per call against 10.1 us for 4 waves plus a merge
+// launch); otherwise 4 waves. 128 / 256 are the reference's threadgroup
+// sizes (2 / 4 waves, separate merge).
 mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t max_keys,
                     uint32_t block_keys, uint32_t threads) {
   p->family = Family::Rows;
   p->kernel = "attn_rows";
-  p->waves = threads == 128 ? 2 : 4;
+  const bool single_decode = threads == 0 && batch == 1 && p->T == 1;
+  p->waves = single_decode ? 8 : threads == 128 ? 2 : 4;
   p->threads = p->waves * 64;
   p->chunk = kernels::rows_chunk(p->G);
   const uint64_t units = batch * p->T * p->Hkv * (p->G / p->chunk);
   p->units = units;
   p->block_keys = block_keys != 0 ? block_keys : default_block(ctx, units, max_keys);
   p->splits = std::max<uint32_t>(1, ceil_div(std::max<uint32_t>(max_keys, 1), p->block_keys));
+  const uint64_t counters = ctx ? ctx->split_counter_count : kernels::kSplitCounters;
+  p->fused = single_decode && p->splits > 1 && units <= counters;
   p->scratch_bytes =
       p->splits > 1 ? units * p->splits * p->chunk * (uint64_t)(p->D + 2) * sizeof(float) : 0;
   if (batch * p->T > 0xffffu || (uint64_t)p->Hkv * (p->G / p->chunk) > 0xffffu)
@@ -167,12 +177,14 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
   if (kind != MI_ATTN_REFERENCE && (!pow2(config->head_dim) || config->head_dim > 256))
     return fail(MI_ERR_SHAPE, "tiled attention requires a power-of-two head_dim <= 256");
   uint32_t flash_block = 0, flash_threads = 0;
+  bool flash_default = false;  // untuned and not explicit: the library default
   if (kind == MI_ATTN_FLASH_DECODE) {
     if (flash_explicit) {
       flash_block = block_keys;
       flash_threads = threads;
     } else {
-      flash_config_for_length(ctx, (uint64_t)kv_length, &flash_block, &flash_threads);
+      flash_default = !flash_config_for_length(ctx, (uint64_t)kv_length, &flash_block,
+                                               &flash_threads);
     }
     if (flash_block != 32 && flash_block != 64 && flash_block != 128 && flash_block != 256)
       return fail(MI_ERR_SHAPE, "flash decode block size must be 32, 64, 128, or 256");
@@ -233,7 +245,9 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
     return MI_OK;
   }
   const uint32_t rows_block = kind == MI_ATTN_FLASH_DECODE ? flash_block : 0;
-  const uint32_t rows_threads = kind == MI_ATTN_FLASH_DECODE ? flash_threads : 256;
+  uint32_t rows_threads = 256;
+  if (kind == MI_ATTN_FLASH_DECODE) rows_threads = flash_default ? 0 : flash_threads;
+  if (kind == MI_ATTN_DECODE_SPLIT_KV) rows_threads = 0;
   st = plan_rows(ctx, &p, 1, available_last, rows_block, rows_threads);
   if (st != MI_OK) return st;
   *plan = p;
@@ -258,6 +272,7 @@ mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
     if ((st = scratch_alloc(batch, p.scratch_bytes, &scratch)) != MI_OK) return st;
   }
   rp.partial = static_cast<float *>(scratch);
+  rp.counters = p.fused ? ctx->split_counters : nullptr;
   rp.block_keys = p.block_keys;
   rp.max_splits = p.splits;
   rp.head_chunks = p.G / p.chunk;
@@ -265,7 +280,7 @@ mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
   st = launch(batch, p.kernel, [&](const kernels::Launch &s) {
     return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Split, s);
   });
-  if (st == MI_OK && p.splits > 1)
+  if (st == MI_OK && p.splits > 1 && !p.fused)
     st = launch(batch, "attn_merge", [&](const kernels::Launch &s) {
       return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Merge, s);
     });

@@ -129,10 +129,14 @@ def test_flash_decode_configuration_is_validated():
             p = plan(q, k, v, cfg, FLASH_DECODE, block, threads)
             assert p["block_keys"] == block and p["block_threads"] == threads
             assert p["splits"] == -(-2048 // block)
-    # untuned default (context.rs:258-267 keeps (64, 256) for Apple GPUs;
-    # 128-key splits measured fastest on MI355X)
+    # untuned default (context.rs:258-267 keeps (64, 256) for Apple GPUs):
+    # 128-key splits, 8 waves per workgroup, merge inside the launch
+    # (measured fastest on MI355X); the configuration query still reports
+    # the nearest reference configuration, (128, 256)
     p = plan(q, k, v, cfg, FLASH_DECODE)
-    assert (p["block_keys"], p["block_threads"]) == (128, 256)
+    assert (p["block_keys"], p["block_threads"]) == (128, 512)
+    p = plan(q, k, v, cfg, DECODE_SPLIT_KV)
+    assert p["block_threads"] == 512
 
 
 def test_flash_decode_accepts_every_gqa_ratio():

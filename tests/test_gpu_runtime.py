@@ -69,9 +69,19 @@ def test_kernel_profiling_records_each_launch(ctx):
         profiles = ctx.take_kernel_profiles()
     finally:
         ctx.set_kernel_profiling(False)
-    # The split-K decode of 1024 keys runs in several blocks, so its merge
-    # pass is a launch of its own.
-    assert [name for name, _ in profiles] == ["attn_rows", "attn_merge", "attn_naive"]
+    # The default decode of 1024 keys runs in several blocks and merges them
+    # inside its one launch; an explicit reference configuration keeps the
+    # merge pass as a launch of its own.
+    assert [name for name, _ in profiles] == ["attn_rows", "attn_naive"]
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        batch.attention_flash_decode_with_configuration(q, k, v, cfg, 128, 256)
+        batch.finish()
+        profiles = ctx.take_kernel_profiles()
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert [name for name, _ in profiles] == ["attn_rows", "attn_merge"]
     assert all(ns > 0 for _, ns in profiles)
 
 
