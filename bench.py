@@ -322,6 +322,68 @@ def bench_prefill(ctx, hip, config, steps, eager):
                    plan=ctx.plan(q, key, value, cfg, kind)["kernel"])
 
 
+# ---------------------------------------------------------------- o_proj --
+
+# The matmul after attention (qwen3.rs:751-752): (label, m, n, k, distinct
+# weights rotated so that the HBM-bound shapes read from HBM rather than the
+# 256 MB MALL, roofline bound).
+O_PROJ = (
+    ("decode o_proj, Qwen3-0.6B: [1, 2048] x [1024, 2048]^T", 1, 1024, 2048, 128, "hbm"),
+    ("batched decode o_proj, Qwen3-8B (c4): [32, 4096] x [4096, 4096]^T", 32, 4096, 4096, 16,
+     "hbm"),
+    ("prefill o_proj, c3 (Qwen3-0.6B): [2048, 2048] x [1024, 2048]^T", 2048, 1024, 2048, 1,
+     "mfma"),
+    ("prefill o_proj, c5 (Qwen3-32B): [4096, 8192] x [5120, 8192]^T", 4096, 5120, 8192, 1,
+     "mfma"),
+)
+
+
+def bench_o_proj(ctx, hip, eager) -> list[dict]:
+    rng = np.random.default_rng(0)
+    results = []
+    for label, m, n, k, rotate, bound in O_PROJ:
+        log(f"o_proj: {label}")
+        x = ctx.tensor((rng.standard_normal((m, k))).astype(np.float16).view(np.uint16))
+        host_w = (rng.standard_normal((n, k)) * k ** -0.5).astype(np.float16).view(np.uint16)
+        weights = [ctx.tensor(host_w) for _ in range(rotate)]
+        out = ctx.empty((m, n))
+
+        def enqueue(batch, i):
+            return batch.matmul(x, weights[i % rotate], out=out)
+
+        b = ctx.begin_batch()
+        enqueue(b, 0)
+        b.finish()
+        steps = max(rotate, 64 if bound == "hbm" else 8)
+        calls, seconds = timed(ctx, hip, enqueue, steps, eager, 2)
+        name, kernel_s, kernels = kernel_profile(ctx, enqueue, max(rotate, 8))
+        entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
+                 "kernel_us": round(kernel_s * 1e6, 3)}
+        if bound == "hbm":
+            nbytes = 2 * (n * k + m * k + m * n)
+            value = nbytes / seconds / 1e9
+            achieved = nbytes / kernel_s / 1e9
+            entry.update({"value": round(value, 2), "unit": "GB/s", "roofline": {
+                "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": nbytes}})
+        else:
+            flops = 2 * m * n * k
+            value = flops / seconds / 1e12
+            achieved = flops / kernel_s / 1e12
+            entry.update({"value": round(value, 2), "unit": "TFLOP/s", "roofline": {
+                "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                "traffic": None, "algorithmic_flops": flops}})
+        log(f"  {entry['value']} {entry['unit']}, {name} {entry['kernel_us']} us")
+        results.append(entry)
+        for w in weights:
+            w.free()
+        x.free()
+        out.free()
+    return results
+
+
 # -------------------------------------------------------------- CPU leg ---
 
 def cpu_baseline(decode_case) -> dict:
@@ -361,9 +423,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workloads", default="c2,c4,c3,c5",
-                    help="comma list of c2 (headline decode), c4, c3, c5; profiling runs "
-                         "select one at a time")
+    ap.add_argument("--workloads", default="c2,c4,c3,c5,o_proj",
+                    help="comma list of c2 (headline decode), c4, c3, c5, o_proj; profiling "
+                         "runs select one at a time")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of HIP graph replays (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -374,7 +436,7 @@ def main() -> int:
               "component in this build; a multi-GPU layout is design-only here", file=sys.stderr)
         return 2
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
-    unknown = set(chosen) - {"c2", "c3", "c4", "c5"}
+    unknown = set(chosen) - {"c2", "c3", "c4", "c5", "o_proj"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -439,6 +501,8 @@ def main() -> int:
                                      "algorithmic_flops": pre["flops"]}})
     if prefill:
         result["prefill"] = prefill
+    if "o_proj" in chosen:
+        result["o_proj"] = bench_o_proj(ctx, hip, args.eager)
     if args.copy_calibration:
         result["copy_calibration"] = copy_calibration(ctx, hip)
     if not args.no_cpu and dc is not None:

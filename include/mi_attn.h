@@ -213,7 +213,8 @@ void *mi_batch_stream(mi_batch *batch);
  * once and replay them. mi_batch_begin_capture opens a batch whose kernels
  * are recorded into a HIP graph (stream capture, relaxed mode) instead of
  * running. Only enqueueing calls belong in it (attention, copy_into_cache,
- * qk_norm_rope_cache, mi_batch_empty); no upload, download or wait.
+ * qk_norm_rope_cache, rms_norm, rope, matmul, mi_batch_empty); no upload,
+ * download or wait.
  * mi_batch_end_capture consumes the batch and returns the graph, which keeps
  * the batch's scratch arena (so tensors leased during capture stay valid and
  * every replay writes the same addresses). Each replay reads and writes the
@@ -324,6 +325,34 @@ mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q,
                                 const mi_tensor *key_cache,
                                 const mi_qk_norm_rope_cache_config *config,
                                 const mi_tensor *q_out);
+
+/* ------------------------------------------------ attention neighbours -- */
+
+/* The steps on either side of attention in Qwen3's forward_layer
+ * (crates/metal-infer-models/src/qwen3.rs:717-752): the unfused Q/K path
+ * (rms_norm, rope, copy_into_cache) and the o_proj matmul of the attention
+ * output. Outputs are caller-provided, like mi_attention's. */
+
+/* CommandBatch::rms_norm (ops.rs:722-755): out = f16(x * scale * weight) per
+ * row of the last dimension, scale = 1 / sqrt(mean(x^2) + epsilon) in f32.
+ * input of rank 1..4 (unit innermost stride), weight [width], out of the
+ * input's shape. */
+mi_status mi_rms_norm(mi_batch *batch, const mi_tensor *input,
+                      const mi_tensor *weight, float epsilon,
+                      const mi_tensor *out);
+/* CommandBatch::rope (ops.rs:882-915): input [T, H, D] with even D; pair
+ * (i, i + D/2) of token t rotated by (offset + t) * theta^(-2i/D). out has
+ * the input's shape. */
+mi_status mi_rope(mi_batch *batch, const mi_tensor *input, uint64_t offset,
+                  float theta, const mi_tensor *out);
+/* CommandBatch::matmul (ops.rs:242-373): out[m, n] = f16(sum_k input[m, k] *
+ * weight[n, k]) with f32 accumulation (weight in the checkpoint's
+ * [out_features, in_features] layout). Up to 8 rows run the library's
+ * HBM-streaming few-row kernel; more rows run a hipBLASLt f16 GEMM with f32
+ * compute, planned once per shape (or the few-row kernel over groups of 8
+ * rows when hipBLASLt has no solution for the shape). */
+mi_status mi_matmul(mi_batch *batch, const mi_tensor *input,
+                    const mi_tensor *weight, const mi_tensor *out);
 
 /* KvCache::new (crates/metal-infer-models/src/qwen3.rs:75-100): one device
  * allocation holding, per layer, key and value as [Hkv, capacity, D]

@@ -1,0 +1,200 @@
+// The attention block's neighbours in the Qwen3 layer: RMSNorm and RoPE of
+// the unfused Q/K path, and the few-row matmul of the decode o_proj.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace mi {
+namespace kernels {
+namespace {
+
+using namespace mi::dev;
+
+__device__ __forceinline__ int64_t row_offset(const RowIndex &ri, uint32_t row) {
+  const uint32_t i2 = row % ri.n2;
+  const uint32_t t = row / ri.n2;
+  return (int64_t)(t / ri.n1) * ri.s0 + (int64_t)(t % ri.n1) * ri.s1 + (int64_t)i2 * ri.s2;
+}
+
+__device__ __forceinline__ uint4 load16(const uint16_t *ptr) {
+  return *reinterpret_cast<const uint4 *>(ptr);
+}
+
+// Eight f16 products of two 16-byte pieces, accumulated in f32.
+__device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
+  acc = dot2(a.x, b.x, acc);
+  acc = dot2(a.y, b.y, acc);
+  acc = dot2(a.z, b.z, acc);
+  return dot2(a.w, b.w, acc);
+}
+
+// rms_norm_f16 (transformer.metal:1318-1340): one wave per row, four rows per
+// workgroup. Pass 1 sums squares (16-byte loads when rows allow), pass 2
+// re-reads the row (an L1/L2 hit) and writes f16(x * scale * w).
+template <bool VEC>
+__global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
+  const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint16_t *x = p.x + row_offset(p.x_rows, row);
+  uint16_t *out = p.out + row_offset(p.o_rows, row);
+  float sum = 0.0f;
+  if constexpr (VEC) {
+    for (uint32_t i = lane * 8; i < p.width; i += 512) {
+      const uint4 v = load16(x + i);
+      sum = dot8(v, v, sum);
+    }
+  } else {
+    for (uint32_t i = lane; i < p.width; i += 64) {
+      const float v = f16_to_f32(x[i]);
+      sum += v * v;
+    }
+  }
+  sum = group_sum<64>(sum);
+  const float scale = 1.0f / sqrtf(sum / (float)p.width + p.epsilon);
+  if constexpr (VEC) {
+    for (uint32_t i = lane * 8; i < p.width; i += 512) {
+      const uint4 v = load16(x + i), w = load16(p.weight + i);
+      const uint32_t vin[4] = {v.x, v.y, v.z, v.w}, win[4] = {w.x, w.y, w.z, w.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = f32_to_f16(lo_f16(vin[j]) * scale * lo_f16(win[j]));
+        const uint16_t hi = f32_to_f16(hi_f16(vin[j]) * scale * hi_f16(win[j]));
+        o[j] = (uint32_t)lo | ((uint32_t)hi << 16);
+      }
+      *reinterpret_cast<uint4 *>(out + i) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  } else {
+    for (uint32_t i = lane; i < p.width; i += 64)
+      out[i] = f32_to_f16(f16_to_f32(x[i]) * scale * f16_to_f32(p.weight[i]));
+  }
+}
+
+// rope_f16 (transformer.metal:1514-1531): one thread per (token, head, pair),
+// pairs (i, i + D/2) rotated by (token + offset) * theta^(-2i/D). The same
+// f32 operations, uncontracted, as the fused Q/K kernel's RoPE step.
+__global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
+#pragma clang fp contract(off)
+  const uint32_t half = p.head_dim / 2;
+  const uint64_t total = (uint64_t)p.tokens * p.heads * half;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t pair = (uint32_t)(i % half);
+    const uint64_t r = i / half;
+    const uint32_t head = (uint32_t)(r % p.heads);
+    const uint32_t token = (uint32_t)(r / p.heads);
+    const uint16_t *x = p.x + (int64_t)token * p.x_tok + (int64_t)head * p.x_head;
+    uint16_t *out = p.out + (int64_t)token * p.o_tok + (int64_t)head * p.o_head;
+    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
+    const float angle = (float)(token + p.offset) * frequency;
+    const float c = cosf(angle), s = sinf(angle);
+    const float a = f16_to_f32(x[pair]), b = f16_to_f32(x[pair + half]);
+    out[pair] = f32_to_f16(a * c - b * s);
+    out[pair + half] = f32_to_f16(a * s + b * c);
+  }
+}
+
+// Few-row matmul (the decode o_proj, matvec_f16 family of
+// transformer.metal:274-400): one wave per weight row (= output column),
+// four per workgroup. Lanes stream the row in 16-byte pieces (64 lanes cover
+// 512 halves), kPieces pieces in flight per lane, and multiply each piece with
+// the same piece of up to ROWS rows of x, which stay cache-resident across the
+// waves. The weight is read from HBM once per ROWS rows of x. Grid
+// (ceil(n / 4), ceil(m / ROWS)).
+template <int ROWS, bool VEC>
+__global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
+  constexpr uint32_t kPieces = 4;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t col = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (col >= p.n) return;
+  const uint32_t r0 = blockIdx.y * ROWS;
+  const uint32_t rows = min((uint32_t)ROWS, p.m - r0);
+  const uint16_t *w = p.w + (int64_t)col * p.w_row;
+  const uint16_t *x = p.x + (int64_t)r0 * p.x_row;
+  float acc[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+  if constexpr (VEC) {
+    const uint32_t pieces = p.k / 8;
+    for (uint32_t base = lane; base < pieces; base += 64 * kPieces) {
+      uint4 wv[kPieces];
+#pragma unroll
+      for (uint32_t u = 0; u < kPieces; ++u) {
+        const uint32_t idx = base + 64 * u;
+        wv[u] = idx < pieces ? load16(w + (size_t)idx * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kPieces; ++u) {
+        const uint32_t idx = base + 64 * u;
+        if (idx < pieces) {
+#pragma unroll
+          for (int r = 0; r < ROWS; ++r)
+            if (r < (int)rows)
+              acc[r] = dot8(wv[u], load16(x + (int64_t)r * p.x_row + (size_t)idx * 8), acc[r]);
+        }
+      }
+    }
+  } else {
+    for (uint32_t i = lane; i < p.k; i += 64) {
+      const float wv = f16_to_f32(w[i]);
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r)
+        if (r < (int)rows) acc[r] += wv * f16_to_f32(x[(int64_t)r * p.x_row + i]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const float total = group_sum<64>(acc[r]);
+    if (lane == (uint32_t)r && r < (int)rows)
+      p.out[(int64_t)(r0 + r) * p.o_row + col] = f32_to_f16(total);
+  }
+}
+
+bool aligned16(const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
+
+bool rows_vector_friendly(const RowIndex &ri) {
+  return ri.s0 % 8 == 0 && ri.s1 % 8 == 0 && ri.s2 % 8 == 0;
+}
+
+template <int ROWS>
+hipError_t dispatch_matvec(const MatvecParams &p, bool vec, dim3 grid, const Launch &l) {
+  if (vec) return dispatch(matvec_kernel<ROWS, true>, grid, dim3(256), 0, l, p);
+  return dispatch(matvec_kernel<ROWS, false>, grid, dim3(256), 0, l, p);
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l) {
+  if (p.rows == 0 || p.width == 0) return no_dispatch(l);
+  const bool vec = p.width % 8 == 0 && rows_vector_friendly(p.x_rows) &&
+                   rows_vector_friendly(p.o_rows) && aligned16(p.x) && aligned16(p.out) &&
+                   aligned16(p.weight);
+  const dim3 grid((p.rows + 3) / 4);
+  if (vec) return dispatch(rms_norm_kernel<true>, grid, dim3(256), 0, l, p);
+  return dispatch(rms_norm_kernel<false>, grid, dim3(256), 0, l, p);
+}
+
+hipError_t launch_rope(const RopeParams &p, const Launch &l) {
+  const uint64_t items = (uint64_t)p.tokens * p.heads * (p.head_dim / 2);
+  if (items == 0) return no_dispatch(l);
+  const uint64_t blocks64 = (items + 255) / 256;
+  const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
+  return dispatch(rope_kernel, dim3(blocks), dim3(256), 0, l, p);
+}
+
+hipError_t launch_matvec(const MatvecParams &p, const Launch &l) {
+  if (p.m == 0 || p.n == 0) return no_dispatch(l);
+  const bool vec = p.k % 8 == 0 && p.x_row % 8 == 0 && p.w_row % 8 == 0 && aligned16(p.x) &&
+                   aligned16(p.w);
+  const uint32_t rows = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : kMatvecRows;
+  const dim3 grid((p.n + 3) / 4, (p.m + rows - 1) / rows);
+  switch (rows) {
+    case 1: return dispatch_matvec<1>(p, vec, grid, l);
+    case 2: return dispatch_matvec<2>(p, vec, grid, l);
+    case 4: return dispatch_matvec<4>(p, vec, grid, l);
+    default: return dispatch_matvec<kMatvecRows>(p, vec, grid, l);
+  }
+}
+
+}  // namespace kernels
+}  // namespace mi

@@ -156,6 +156,52 @@ constexpr uint32_t kNaiveLdsKeys = 12288;
 hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l);
 hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l);
 
+// Rows of up to four dimensions addressed as (i0, i1, i2) over the leading
+// dimensions (n1, n2 the inner two; unused ones have size 1), each row
+// `width` elements at unit stride.
+struct RowIndex {
+  uint32_t n1, n2;
+  int64_t s0, s1, s2;
+};
+
+// RMSNorm over the last dimension: out = x * rsqrt(mean(x^2) + eps) * w.
+struct RmsNormParams {
+  const uint16_t *x;
+  RowIndex x_rows;
+  const uint16_t *weight;
+  uint16_t *out;
+  RowIndex o_rows;
+  uint32_t rows, width;
+  float epsilon;
+};
+
+// RoPE of [T, H, D] (pairs (i, i + D/2)) at position offset + token.
+struct RopeParams {
+  const uint16_t *x;
+  int64_t x_tok, x_head;
+  uint16_t *out;
+  int64_t o_tok, o_head;
+  uint32_t tokens, heads, head_dim, offset;
+  float theta;
+};
+
+// out[m, n] = x[m, k] . w[n, k]^T with f32 accumulation, for few rows of x:
+// the weight is streamed from HBM once per kMatvecRows rows of x.
+struct MatvecParams {
+  const uint16_t *x;
+  int64_t x_row;
+  const uint16_t *w;
+  int64_t w_row;
+  uint16_t *out;
+  int64_t o_row;
+  uint32_t m, n, k;
+};
+constexpr uint32_t kMatvecRows = 8;
+
+hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l);
+hipError_t launch_rope(const RopeParams &p, const Launch &l);
+hipError_t launch_matvec(const MatvecParams &p, const Launch &l);
+
 // Rows of the packed (token, head-in-group) M dimension per prefill
 // workgroup, and keys per KV tile.
 constexpr uint32_t kPrefillBlockM = 128;

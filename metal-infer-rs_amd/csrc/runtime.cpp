@@ -268,6 +268,7 @@ void mi_context_destroy(mi_context *ctx) {
     cache->ctx = nullptr;
   }
   hipFree(ctx->split_counters);
+  mi::release_gemm(ctx);
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }

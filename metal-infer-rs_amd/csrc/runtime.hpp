@@ -22,6 +22,8 @@ struct mi_kv_cache;
 
 namespace mi {
 
+struct GemmState;
+
 // Records `message` as this thread's last error and returns `status`.
 mi_status fail(mi_status status, const std::string &message);
 mi_status hip_fail(mi_status status, const char *what, hipError_t err);
@@ -87,7 +89,13 @@ struct Context {
   std::unordered_set<mi_kv_cache *> caches;
   // Live captured graphs (same ownership rule as caches).
   std::unordered_set<mi_graph *> graphs;
+  // hipBLASLt handle and per-shape GEMM plans, made at the first matmul
+  // with more rows than the few-row kernel takes.
+  GemmState *gemm = nullptr;
 };
+
+// Frees the context's hipBLASLt handle and plans (after its stream drained).
+void release_gemm(Context *ctx);
 
 struct LaunchRecord {
   std::string kernel;

@@ -145,6 +145,9 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into_cache": (ctypes.c_int, [ctypes.c_void_p, T, T, ctypes.c_uint64]),
         "mi_qk_norm_rope_cache": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T, T,
                                                  _P(QkNormRopeCacheConfig), T]),
+        "mi_rms_norm": (ctypes.c_int, [ctypes.c_void_p, T, T, ctypes.c_float, T]),
+        "mi_rope": (ctypes.c_int, [ctypes.c_void_p, T, ctypes.c_uint64, ctypes.c_float, T]),
+        "mi_matmul": (ctypes.c_int, [ctypes.c_void_p, T, T, T]),
         "mi_kv_cache_create": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_uint32, ctypes.c_uint64,
                                               _P(ctypes.c_void_p)]),
@@ -386,6 +389,24 @@ class Context:
         batch.copy_into_cache(source, cache, offset)
         batch.finish()
 
+    def rms_norm(self, x, weight, epsilon: float) -> Tensor:
+        batch = self.begin_batch()
+        out = batch.rms_norm(x, weight, epsilon)
+        batch.finish()
+        return out
+
+    def rope(self, x, offset: int, theta: float) -> Tensor:
+        batch = self.begin_batch()
+        out = batch.rope(x, offset, theta)
+        batch.finish()
+        return out
+
+    def matmul(self, x, weight) -> Tensor:
+        batch = self.begin_batch()
+        out = batch.matmul(x, weight)
+        batch.finish()
+        return out
+
 
 def plan(q: Tensor, k: Tensor, v: Tensor, config: AttentionConfig, kind: int,
          block_keys: int = 0, threads: int = 0, ctx: Context | None = None) -> dict:
@@ -482,6 +503,27 @@ class Batch:
             self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(q_weight.desc),
             ctypes.byref(k_weight.desc), ctypes.byref(key_cache.desc), ctypes.byref(config),
             ctypes.byref(out.desc)))
+        return out
+
+    def rms_norm(self, x: Tensor, weight: Tensor, epsilon: float, out=None) -> Tensor:
+        out = self._out(x.shape, out)
+        _check(lib().mi_rms_norm(self.handle, ctypes.byref(x.desc), ctypes.byref(weight.desc),
+                                 epsilon, ctypes.byref(out.desc)))
+        return out
+
+    def rope(self, x: Tensor, offset: int, theta: float, out=None) -> Tensor:
+        out = self._out(x.shape, out)
+        _check(lib().mi_rope(self.handle, ctypes.byref(x.desc), offset, theta,
+                             ctypes.byref(out.desc)))
+        return out
+
+    def matmul(self, x: Tensor, weight: Tensor, out=None) -> Tensor:
+        if out is None:
+            shape = (x.shape[0], weight.shape[0]) if len(x.shape) == 2 and len(weight.shape) == 2 \
+                else (1,)
+            out = self.empty(shape)
+        _check(lib().mi_matmul(self.handle, ctypes.byref(x.desc), ctypes.byref(weight.desc),
+                               ctypes.byref(out.desc)))
         return out
 
     def commit(self) -> "Batch":

@@ -373,3 +373,80 @@ int orc_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *q_w,
   }
   return 0;
 }
+
+/* ------------------------------------------------ attention neighbours -- */
+
+int orc_rms_norm(const uint16_t *x, const uint16_t *w, uint64_t rows,
+                 uint32_t width, float epsilon, uint16_t *out, float *out_f32) {
+  if (width == 0)
+    return -1;
+  for (uint64_t row = 0; row < rows; ++row) {
+    const uint16_t *in = x + row * width;
+    /* transformer.metal:1330-1337 (one running sum instead of 32 lane sums
+     * and a SIMD reduction: the same value up to f32 summation order). */
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < width; ++i) {
+      float value = orc_f16_to_f32(in[i]);
+      sum += value * value;
+    }
+    float scale = 1.0f / sqrtf(sum / (float)width + epsilon);
+    /* :1338-1339 */
+    for (uint32_t i = 0; i < width; ++i) {
+      float value = orc_f16_to_f32(in[i]) * scale * orc_f16_to_f32(w[i]);
+      out[row * width + i] = orc_f32_to_f16(value);
+      if (out_f32)
+        out_f32[row * width + i] = value;
+    }
+  }
+  return 0;
+}
+
+int orc_rope(const uint16_t *x, uint32_t tokens, uint32_t heads,
+             uint32_t head_dim, uint32_t offset, float theta, uint16_t *out) {
+  if (head_dim == 0 || head_dim % 2 != 0)
+    return -1;
+  const uint32_t half = head_dim / 2;
+  for (uint32_t token = 0; token < tokens; ++token) {
+    for (uint32_t head = 0; head < heads; ++head) {
+      /* transformer.metal:1522-1530 */
+      size_t base = ((size_t)token * heads + head) * head_dim;
+      for (uint32_t pair = 0; pair < half; ++pair) {
+        uint32_t second = pair + half;
+        float frequency = powf(theta, -(float)(pair * 2) / (float)head_dim);
+        float angle = (float)(token + offset) * frequency;
+        float a = orc_f16_to_f32(x[base + pair]);
+        float b = orc_f16_to_f32(x[base + second]);
+        float c = cosf(angle), s = sinf(angle);
+        out[base + pair] = orc_f32_to_f16(a * c - b * s);
+        out[base + second] = orc_f32_to_f16(a * s + b * c);
+      }
+    }
+  }
+  return 0;
+}
+
+int orc_matmul(const uint16_t *x, const uint16_t *w, uint32_t m, uint32_t n,
+               uint32_t k, uint16_t *out, float *out_f32, int threads) {
+  if (threads <= 0)
+    threads = omp_get_max_threads();
+  /* transformer.metal:77-92: one f32 sum per output, k ascending. */
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (int64_t i = 0; i < (int64_t)m; ++i) {
+    float *row = malloc(sizeof(float) * (size_t)k);
+    if (row == NULL)
+      abort();
+    for (uint32_t c = 0; c < k; ++c)
+      row[c] = orc_f16_to_f32(x[(size_t)i * k + c]);
+    for (uint32_t j = 0; j < n; ++j) {
+      const uint16_t *wr = w + (size_t)j * k;
+      float sum = 0.0f;
+      for (uint32_t c = 0; c < k; ++c)
+        sum += row[c] * orc_f16_to_f32(wr[c]);
+      out[(size_t)i * n + j] = orc_f32_to_f16(sum);
+      if (out_f32)
+        out_f32[(size_t)i * n + j] = sum;
+    }
+    free(row);
+  }
+  return 0;
+}

@@ -93,6 +93,26 @@ int orc_qk_norm_rope(const uint16_t *q, const uint16_t *k, const uint16_t *q_w,
                      float theta, float epsilon, uint16_t *q_out,
                      uint16_t *key_out);
 
+/* Restatement of rms_norm_f16 (transformer.metal:1318-1340) for `rows`
+ * contiguous rows of `width`: scale = 1 / sqrt(sum(x^2) / width + epsilon)
+ * with the squares summed in ascending order in f32, out = f16(x * scale *
+ * w). out_f32 (optional) receives the unrounded values. */
+int orc_rms_norm(const uint16_t *x, const uint16_t *w, uint64_t rows,
+                 uint32_t width, float epsilon, uint16_t *out, float *out_f32);
+
+/* Restatement of rope_f16 (transformer.metal:1514-1531) on contiguous
+ * [tokens, heads, head_dim]: pair (i, i + D/2) of token t rotated by
+ * (t + offset) * theta^(-2i/D). */
+int orc_rope(const uint16_t *x, uint32_t tokens, uint32_t heads,
+             uint32_t head_dim, uint32_t offset, float theta, uint16_t *out);
+
+/* Restatement of matmul_f16 (transformer.metal:70-93): out[i][j] =
+ * f16(sum_k f32(x[i][k]) * f32(w[j][k])), k ascending, for contiguous x
+ * [m, k] and w [n, k]. out_f32 (optional) receives the unrounded sums.
+ * Rows of out are spread over `threads` OpenMP threads (0 = default). */
+int orc_matmul(const uint16_t *x, const uint16_t *w, uint32_t m, uint32_t n,
+               uint32_t k, uint16_t *out, float *out_f32, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,6 +85,15 @@ def lib() -> ctypes.CDLL:
             _u16p, _u16p, _u16p, _u16p, ctypes.c_uint32, ctypes.c_uint32,
             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
             ctypes.c_float, _u16p, _u16p]
+        handle.orc_rms_norm.restype = ctypes.c_int
+        handle.orc_rms_norm.argtypes = [_u16p, _u16p, ctypes.c_uint64, ctypes.c_uint32,
+                                        ctypes.c_float, _u16p, _f32p]
+        handle.orc_rope.restype = ctypes.c_int
+        handle.orc_rope.argtypes = [_u16p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_uint32, ctypes.c_float, _u16p]
+        handle.orc_matmul.restype = ctypes.c_int
+        handle.orc_matmul.argtypes = [_u16p, _u16p, ctypes.c_uint32, ctypes.c_uint32,
+                                      ctypes.c_uint32, _u16p, _f32p, ctypes.c_int]
         _lib = handle
     return _lib
 
@@ -206,3 +215,45 @@ def qk_norm_rope(q, k, q_weight, k_weight, *, offset: int, theta: float, epsilon
     if rc != 0:
         raise ValueError("oracle rejected the Q/K transform geometry")
     return q_out, k_out
+
+
+def rms_norm(x, weight, *, epsilon: float):
+    """Restatement of rms_norm_f16 (transformer.metal:1318-1340) over the last
+    dimension. Returns (f16 bits, unrounded f32), both of x's shape."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(weight, dtype=np.uint16)
+    width = x.shape[-1]
+    out = np.empty_like(x)
+    out32 = np.empty(x.shape, dtype=np.float32)
+    rc = lib().orc_rms_norm(x.ctypes.data_as(_u16p), w.ctypes.data_as(_u16p), x.size // width,
+                            width, epsilon, out.ctypes.data_as(_u16p), out32.ctypes.data_as(_f32p))
+    if rc != 0:
+        raise ValueError("oracle rejected the RMSNorm geometry")
+    return out, out32
+
+
+def rope(x, *, offset: int, theta: float):
+    """Restatement of rope_f16 (transformer.metal:1514-1531) on [T, H, D]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    T, h, d = x.shape
+    out = np.empty_like(x)
+    rc = lib().orc_rope(x.ctypes.data_as(_u16p), T, h, d, offset, theta, out.ctypes.data_as(_u16p))
+    if rc != 0:
+        raise ValueError("oracle rejected the RoPE geometry")
+    return out
+
+
+def matmul(x, weight, threads: int | None = None):
+    """Restatement of matmul_f16 (transformer.metal:70-93): x [m, k] times
+    weight [n, k] transposed. Returns (f16 bits [m, n], unrounded f32)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(weight, dtype=np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    assert w.shape[1] == k
+    out = np.empty((m, n), dtype=np.uint16)
+    out32 = np.empty((m, n), dtype=np.float32)
+    lib().orc_matmul(x.ctypes.data_as(_u16p), w.ctypes.data_as(_u16p), m, n, k,
+                     out.ctypes.data_as(_u16p), out32.ctypes.data_as(_f32p),
+                     default_threads() if threads is None else threads)
+    return out, out32
