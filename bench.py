@@ -217,7 +217,7 @@ def bench_decode(ctx, hip, steps, warmup, eager):
 
 def bench_decode_step(ctx, hip, steps):
     """One c2-sized decode step in qwen3.rs:704-750 order (Q/K norm + RoPE with
-    K into the cache, V append, FlashDecode over the prefix: four kernels),
+    K into the cache, V append, FlashDecode over the prefix: three kernels),
     replayed from a graph captured with the library's capture API, against
     the same step enqueued eagerly. Seconds per step for each."""
     c = workloads.case(2)
@@ -261,7 +261,7 @@ def bench_decode_step(ctx, hip, steps):
     graph.destroy()
     cache.close()
     return {"workload": "c2 decode step: qk_norm_rope_cache + copy_into_cache + FlashDecode "
-                        "(4 kernels), same cache slot every step",
+                        "(3 kernels), same cache slot every step",
             "graph_us": round(ms.value * 1e3 / steps, 3), "eager_us": round(eager * 1e6, 3)}
 
 
