@@ -86,7 +86,7 @@ bool flash_config_for_length(const Context *ctx, uint64_t length, uint32_t *bloc
 // launch); otherwise 4 waves. 128 / 256 are the reference's threadgroup
 // sizes (2 / 4 waves, separate merge).
 mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t max_keys,
-                    uint32_t block_keys, uint32_t threads) {
+                    uint32_t block_keys, uint32_t threads, bool batched = false) {
   p->family = Family::Rows;
   p->kernel = "attn_rows";
   const bool single_decode = threads == 0 && batch == 1 && p->T == 1;
@@ -98,7 +98,10 @@ mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t ma
   p->block_keys = block_keys != 0 ? block_keys : default_block(ctx, units, max_keys);
   p->splits = std::max<uint32_t>(1, ceil_div(std::max<uint32_t>(max_keys, 1), p->block_keys));
   const uint64_t counters = ctx ? ctx->split_counter_count : kernels::kSplitCounters;
-  p->fused = single_decode && p->splits > 1 && units <= counters;
+  // The batched decode merges inside its launch too (4 waves; with the
+  // streamed K/V loads measured 2.5% faster at 32 sequences than a merge
+  // launch).
+  p->fused = (single_decode || batched) && p->splits > 1 && units <= counters;
   p->scratch_bytes =
       p->splits > 1 ? units * p->splits * p->chunk * (uint64_t)(p->D + 2) * sizeof(float) : 0;
   if (batch * p->T > 0xffffu || (uint64_t)p->Hkv * (p->G / p->chunk) > 0xffffu)
@@ -459,7 +462,8 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   // large power of two, so the workgroups, which stream in lockstep, keep
   // landing on the same HBM channels.
   if (block_keys == 0) block_keys = std::min<uint32_t>(768, std::max<uint32_t>(64, p.L));
-  if ((st = plan_rows(batch->ctx, &p, (uint64_t)B, p.L, block_keys, 256)) != MI_OK) return st;
+  if ((st = plan_rows(batch->ctx, &p, (uint64_t)B, p.L, block_keys, 256, true)) != MI_OK)
+    return st;
   kernels::RowsParams rp{};
   rp.q = static_cast<const uint16_t *>(q->data);
   rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
