@@ -19,6 +19,13 @@ __device__ __forceinline__ uint4 load16(const uint16_t *ptr) {
   return *reinterpret_cast<const uint4 *>(ptr);
 }
 
+// Weights are streamed (each byte read once per call): non-temporal loads.
+__device__ __forceinline__ uint4 load16_stream(const uint16_t *ptr) {
+  typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+  const u4_t x = __builtin_nontemporal_load(reinterpret_cast<const u4_t *>(ptr));
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 // Eight f16 products of two 16-byte pieces, accumulated in f32.
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
   acc = dot2(a.x, b.x, acc);
@@ -121,7 +128,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecParams p) {
 #pragma unroll
       for (uint32_t u = 0; u < kPieces; ++u) {
         const uint32_t idx = base + 64 * u;
-        wv[u] = idx < pieces ? load16(w + (size_t)idx * 8) : make_uint4(0, 0, 0, 0);
+        wv[u] = idx < pieces ? load16_stream(w + (size_t)idx * 8) : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (uint32_t u = 0; u < kPieces; ++u) {
