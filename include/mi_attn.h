@@ -213,8 +213,8 @@ void *mi_batch_stream(mi_batch *batch);
  * once and replay them. mi_batch_begin_capture opens a batch whose kernels
  * are recorded into a HIP graph (stream capture, relaxed mode) instead of
  * running. Only enqueueing calls belong in it (attention, copy_into_cache,
- * qk_norm_rope_cache, rms_norm, rope, matmul, mi_batch_empty); no upload,
- * download or wait.
+ * qk_norm_rope_cache(_value), rms_norm, rope, matmul, mi_batch_empty); no
+ * upload, download or wait.
  * mi_batch_end_capture consumes the batch and returns the graph, which keeps
  * the batch's scratch arena (so tensors leased during capture stay valid and
  * every replay writes the same addresses). Each replay reads and writes the
@@ -325,6 +325,22 @@ mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q,
                                 const mi_tensor *key_cache,
                                 const mi_qk_norm_rope_cache_config *config,
                                 const mi_tensor *q_out);
+
+/* qk_norm_rope_cache followed by copy_into_cache of the value rows, in one
+ * launch. No counterpart in the reference: forward_layer issues the two back
+ * to back for every layer and token (crates/metal-infer-models/src/
+ * qwen3.rs:704-728), and on MI355X one kernel fewer per layer shortens a
+ * captured decode step. value [T, Hkv, D] goes to value_cache
+ * [capacity, Hkv, D] at config->offset; every other argument, and every
+ * error, is as for mi_qk_norm_rope_cache and mi_copy_into_cache. */
+mi_status mi_qk_norm_rope_cache_value(mi_batch *batch, const mi_tensor *q,
+                                      const mi_tensor *k, const mi_tensor *value,
+                                      const mi_tensor *q_weight,
+                                      const mi_tensor *k_weight,
+                                      const mi_tensor *key_cache,
+                                      const mi_tensor *value_cache,
+                                      const mi_qk_norm_rope_cache_config *config,
+                                      const mi_tensor *q_out);
 
 /* ------------------------------------------------ attention neighbours -- */
 

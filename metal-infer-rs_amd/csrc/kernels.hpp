@@ -104,6 +104,12 @@ struct QkNormRopeParams {
   int64_t qo_tok, qo_head;
   uint16_t *cache;
   int64_t c_pos, c_head;
+  // Optional value append (v != null): rows v[T, Hkv, D] are copied to
+  // v_cache at position offset + token by workgroups after the Q/K rows.
+  const uint16_t *v;
+  int64_t v_tok, v_head;
+  uint16_t *v_cache;
+  int64_t vc_pos, vc_head;
   uint32_t tokens, q_heads, kv_heads, head_dim, offset;
   float theta, epsilon;
 };

@@ -374,6 +374,78 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
   return run_rows(batch, p, rp);
 }
 
+// copy_into_cache's validation (ops.rs:1249-1285): source [T, H, D] into
+// cache [C, H, D] at `offset`.
+mi_status check_kv_append(const mi_tensor *source, const mi_tensor *cache, uint64_t offset) {
+  mi_status st;
+  if ((st = require_f16(source)) != MI_OK || (st = require_f16(cache)) != MI_OK) return st;
+  if (source->rank != 3) return fail(MI_ERR_SHAPE, "KV source must have rank 3");
+  if (cache->rank != 3) return fail(MI_ERR_SHAPE, "KV cache must have rank 3");
+  if (source->shape[1] != cache->shape[1] || source->shape[2] != cache->shape[2])
+    return fail(MI_ERR_SHAPE, "KV source/cache shapes are incompatible");
+  if (offset + (uint64_t)source->shape[0] > (uint64_t)cache->shape[0])
+    return fail(MI_ERR_SHAPE, "KV cache capacity exceeded");
+  if (source->stride[2] != 1 || cache->stride[2] != 1)
+    return fail(MI_ERR_SHAPE, "KV rows need a unit innermost stride");
+  uint32_t tmp;
+  if ((st = to_u32(source->shape[0], "tokens", &tmp)) != MI_OK) return st;
+  if ((st = to_u32((int64_t)offset, "offset", &tmp)) != MI_OK) return st;
+  if ((st = to_u32(source->shape[1] * source->shape[2], "stride", &tmp)) != MI_OK) return st;
+  return MI_OK;
+}
+
+// qk_norm_rope_cache's validation (ops.rs:917-977) and its kernel parameters.
+mi_status prepare_qk_norm_rope(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                               const mi_tensor *q_weight, const mi_tensor *k_weight,
+                               const mi_tensor *key_cache,
+                               const mi_qk_norm_rope_cache_config *config,
+                               const mi_tensor *q_out, kernels::QkNormRopeParams *out) {
+  if (batch == nullptr || q == nullptr || k == nullptr || q_weight == nullptr ||
+      k_weight == nullptr || key_cache == nullptr || config == nullptr || q_out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
+  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
+  mi_status st;
+  if ((st = require_f16(q)) != MI_OK || (st = require_f16(k)) != MI_OK ||
+      (st = require_f16(q_weight)) != MI_OK || (st = require_f16(k_weight)) != MI_OK ||
+      (st = require_f16(key_cache)) != MI_OK)
+    return st;
+  if (q->rank != 3) return fail(MI_ERR_SHAPE, "query must have rank 3");
+  if (k->rank != 3) return fail(MI_ERR_SHAPE, "key must have rank 3");
+  if (key_cache->rank != 3) return fail(MI_ERR_SHAPE, "key cache must have rank 3");
+  const int64_t tokens = q->shape[0], head_dim = q->shape[2];
+  if (tokens != k->shape[0] || head_dim != k->shape[2] || k->shape[1] != key_cache->shape[1] ||
+      head_dim != key_cache->shape[2] || q_weight->rank != 1 || q_weight->shape[0] != head_dim ||
+      k_weight->rank != 1 || k_weight->shape[0] != head_dim)
+    return fail(MI_ERR_SHAPE, "Q/K transform tensor shapes are incompatible");
+  if (head_dim % 2 != 0 || (uint64_t)config->offset + (uint64_t)tokens > (uint64_t)key_cache->shape[0])
+    return fail(MI_ERR_SHAPE, "Q/K transform has invalid head_dim or cache offset");
+  if ((st = require_f16(q_out)) != MI_OK) return st;
+  if (q_out->rank != 3 || q_out->shape[0] != q->shape[0] || q_out->shape[1] != q->shape[1] ||
+      q_out->shape[2] != q->shape[2])
+    return fail(MI_ERR_SHAPE, "Q/K transform output must have the query's shape");
+  if (q->stride[2] != 1 || k->stride[2] != 1 || key_cache->stride[2] != 1 ||
+      q_out->stride[2] != 1 || q_weight->stride[0] != 1 || k_weight->stride[0] != 1)
+    return fail(MI_ERR_SHAPE, "Q/K transform tensors need a unit innermost stride");
+  kernels::QkNormRopeParams &qp = *out;
+  qp = kernels::QkNormRopeParams{};
+  if ((st = to_u32(tokens, "tokens", &qp.tokens)) != MI_OK) return st;
+  if ((st = to_u32(q->shape[1], "query heads", &qp.q_heads)) != MI_OK) return st;
+  if ((st = to_u32(k->shape[1], "KV heads", &qp.kv_heads)) != MI_OK) return st;
+  if ((st = to_u32(head_dim, "head dim", &qp.head_dim)) != MI_OK) return st;
+  qp.offset = config->offset;
+  qp.theta = config->theta;
+  qp.epsilon = config->epsilon;
+  qp.q = static_cast<const uint16_t *>(q->data), qp.q_tok = q->stride[0], qp.q_head = q->stride[1];
+  qp.k = static_cast<const uint16_t *>(k->data), qp.k_tok = k->stride[0], qp.k_head = k->stride[1];
+  qp.q_weight = static_cast<const uint16_t *>(q_weight->data);
+  qp.k_weight = static_cast<const uint16_t *>(k_weight->data);
+  qp.q_out = static_cast<uint16_t *>(q_out->data);
+  qp.qo_tok = q_out->stride[0], qp.qo_head = q_out->stride[1];
+  qp.cache = static_cast<uint16_t *>(key_cache->data);
+  qp.c_pos = key_cache->stride[0], qp.c_head = key_cache->stride[1];
+  return MI_OK;
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -589,20 +661,10 @@ mi_status mi_copy_into_cache(mi_batch *batch, const mi_tensor *source, const mi_
     return fail(MI_ERR_INVALID_ARGUMENT, "null batch or tensor");
   if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
   mi_status st;
-  if ((st = require_f16(source)) != MI_OK || (st = require_f16(cache)) != MI_OK) return st;
-  if (source->rank != 3) return fail(MI_ERR_SHAPE, "KV source must have rank 3");
-  if (cache->rank != 3) return fail(MI_ERR_SHAPE, "KV cache must have rank 3");
-  if (source->shape[1] != cache->shape[1] || source->shape[2] != cache->shape[2])
-    return fail(MI_ERR_SHAPE, "KV source/cache shapes are incompatible");
-  if (offset + (uint64_t)source->shape[0] > (uint64_t)cache->shape[0])
-    return fail(MI_ERR_SHAPE, "KV cache capacity exceeded");
-  if (source->stride[2] != 1 || cache->stride[2] != 1)
-    return fail(MI_ERR_SHAPE, "KV rows need a unit innermost stride");
+  if ((st = check_kv_append(source, cache, offset)) != MI_OK) return st;
   kernels::CopyKvParams cp{};
-  uint32_t tmp;
-  if ((st = to_u32(source->shape[0], "tokens", &cp.tokens)) != MI_OK) return st;
-  if ((st = to_u32((int64_t)offset, "offset", &cp.offset)) != MI_OK) return st;
-  if ((st = to_u32(source->shape[1] * source->shape[2], "stride", &tmp)) != MI_OK) return st;
+  cp.tokens = (uint32_t)source->shape[0];
+  cp.offset = (uint32_t)offset;
   cp.src = static_cast<const uint16_t *>(source->data);
   cp.s_tok = source->stride[0], cp.s_head = source->stride[1];
   cp.dst = static_cast<uint16_t *>(cache->data);
@@ -617,48 +679,32 @@ mi_status mi_qk_norm_rope_cache(mi_batch *batch, const mi_tensor *q, const mi_te
                                 const mi_tensor *key_cache,
                                 const mi_qk_norm_rope_cache_config *config,
                                 const mi_tensor *q_out) {
-  if (batch == nullptr || q == nullptr || k == nullptr || q_weight == nullptr ||
-      k_weight == nullptr || key_cache == nullptr || config == nullptr || q_out == nullptr)
+  kernels::QkNormRopeParams qp;
+  mi_status st = prepare_qk_norm_rope(batch, q, k, q_weight, k_weight, key_cache, config, q_out, &qp);
+  if (st != MI_OK) return st;
+  return launch(batch, "qk_norm_rope_cache",
+                [&](const kernels::Launch &s) { return kernels::launch_qk_norm_rope(qp, s); });
+}
+
+mi_status mi_qk_norm_rope_cache_value(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                                      const mi_tensor *value, const mi_tensor *q_weight,
+                                      const mi_tensor *k_weight, const mi_tensor *key_cache,
+                                      const mi_tensor *value_cache,
+                                      const mi_qk_norm_rope_cache_config *config,
+                                      const mi_tensor *q_out) {
+  if (value == nullptr || value_cache == nullptr)
     return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
-  if (batch->committed) return fail(MI_ERR_RESOURCE, "batch was already committed");
-  mi_status st;
-  if ((st = require_f16(q)) != MI_OK || (st = require_f16(k)) != MI_OK ||
-      (st = require_f16(q_weight)) != MI_OK || (st = require_f16(k_weight)) != MI_OK ||
-      (st = require_f16(key_cache)) != MI_OK)
-    return st;
-  if (q->rank != 3) return fail(MI_ERR_SHAPE, "query must have rank 3");
-  if (k->rank != 3) return fail(MI_ERR_SHAPE, "key must have rank 3");
-  if (key_cache->rank != 3) return fail(MI_ERR_SHAPE, "key cache must have rank 3");
-  const int64_t tokens = q->shape[0], head_dim = q->shape[2];
-  if (tokens != k->shape[0] || head_dim != k->shape[2] || k->shape[1] != key_cache->shape[1] ||
-      head_dim != key_cache->shape[2] || q_weight->rank != 1 || q_weight->shape[0] != head_dim ||
-      k_weight->rank != 1 || k_weight->shape[0] != head_dim)
-    return fail(MI_ERR_SHAPE, "Q/K transform tensor shapes are incompatible");
-  if (head_dim % 2 != 0 || (uint64_t)config->offset + (uint64_t)tokens > (uint64_t)key_cache->shape[0])
-    return fail(MI_ERR_SHAPE, "Q/K transform has invalid head_dim or cache offset");
-  if ((st = require_f16(q_out)) != MI_OK) return st;
-  if (q_out->rank != 3 || q_out->shape[0] != q->shape[0] || q_out->shape[1] != q->shape[1] ||
-      q_out->shape[2] != q->shape[2])
-    return fail(MI_ERR_SHAPE, "Q/K transform output must have the query's shape");
-  if (q->stride[2] != 1 || k->stride[2] != 1 || key_cache->stride[2] != 1 ||
-      q_out->stride[2] != 1 || q_weight->stride[0] != 1 || k_weight->stride[0] != 1)
-    return fail(MI_ERR_SHAPE, "Q/K transform tensors need a unit innermost stride");
-  kernels::QkNormRopeParams qp{};
-  if ((st = to_u32(tokens, "tokens", &qp.tokens)) != MI_OK) return st;
-  if ((st = to_u32(q->shape[1], "query heads", &qp.q_heads)) != MI_OK) return st;
-  if ((st = to_u32(k->shape[1], "KV heads", &qp.kv_heads)) != MI_OK) return st;
-  if ((st = to_u32(head_dim, "head dim", &qp.head_dim)) != MI_OK) return st;
-  qp.offset = config->offset;
-  qp.theta = config->theta;
-  qp.epsilon = config->epsilon;
-  qp.q = static_cast<const uint16_t *>(q->data), qp.q_tok = q->stride[0], qp.q_head = q->stride[1];
-  qp.k = static_cast<const uint16_t *>(k->data), qp.k_tok = k->stride[0], qp.k_head = k->stride[1];
-  qp.q_weight = static_cast<const uint16_t *>(q_weight->data);
-  qp.k_weight = static_cast<const uint16_t *>(k_weight->data);
-  qp.q_out = static_cast<uint16_t *>(q_out->data);
-  qp.qo_tok = q_out->stride[0], qp.qo_head = q_out->stride[1];
-  qp.cache = static_cast<uint16_t *>(key_cache->data);
-  qp.c_pos = key_cache->stride[0], qp.c_head = key_cache->stride[1];
+  kernels::QkNormRopeParams qp;
+  mi_status st = prepare_qk_norm_rope(batch, q, k, q_weight, k_weight, key_cache, config, q_out, &qp);
+  if (st != MI_OK) return st;
+  if ((st = check_kv_append(value, value_cache, config->offset)) != MI_OK) return st;
+  if (value->shape[0] != q->shape[0] || value->shape[1] != k->shape[1] ||
+      value->shape[2] != k->shape[2])
+    return fail(MI_ERR_SHAPE, "value rows must have the key's shape");
+  qp.v = static_cast<const uint16_t *>(value->data);
+  qp.v_tok = value->stride[0], qp.v_head = value->stride[1];
+  qp.v_cache = static_cast<uint16_t *>(value_cache->data);
+  qp.vc_pos = value_cache->stride[0], qp.vc_head = value_cache->stride[1];
   return launch(batch, "qk_norm_rope_cache",
                 [&](const kernels::Launch &s) { return kernels::launch_qk_norm_rope(qp, s); });
 }

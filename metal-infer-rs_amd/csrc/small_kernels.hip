@@ -93,10 +93,21 @@ __global__ __launch_bounds__(256) void copy_kv_kernel(CopyKvParams p) {
 
 // qk_norm_rope_cache_f16 (transformer.metal:1533-1577): one wave per
 // (token, head) row; query rows first, then key rows, which are written
-// straight into the cache at position offset + token.
+// straight into the cache at position offset + token. With p.v set, a last
+// group of rows copies the value rows into their cache (copy_kv_f16,
+// transformer.metal:2318-2325) in the same launch.
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(QkNormRopeParams p) {
 #pragma clang fp contract(off)
   const uint32_t group = blockIdx.x;
+  const uint32_t qk_rows = p.tokens * (p.q_heads + p.kv_heads);
+  if (group >= qk_rows) {
+    const uint32_t row = group - qk_rows;
+    const uint32_t token = row / p.kv_heads, head = row % p.kv_heads;
+    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head;
+    uint16_t *dst = p.v_cache + (int64_t)(p.offset + token) * p.vc_pos + (int64_t)head * p.vc_head;
+    for (uint32_t i = threadIdx.x; i < p.head_dim; i += 64) dst[i] = src[i];
+    return;
+  }
   const uint32_t query_rows = p.tokens * p.q_heads;
   const bool is_query = group < query_rows;
   const uint32_t row = is_query ? group : group - query_rows;
@@ -161,7 +172,8 @@ hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l) {
 }
 
 hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
-  const uint32_t groups = p.tokens * (p.q_heads + p.kv_heads);
+  const uint32_t groups =
+      p.tokens * (p.q_heads + p.kv_heads) + (p.v != nullptr ? p.tokens * p.kv_heads : 0u);
   if (groups == 0) return no_dispatch(l);
   return dispatch(qk_norm_rope_kernel, dim3(groups), dim3(64), 0, l, p);
 }

@@ -145,6 +145,8 @@ def _load() -> ctypes.CDLL:
         "mi_copy_into_cache": (ctypes.c_int, [ctypes.c_void_p, T, T, ctypes.c_uint64]),
         "mi_qk_norm_rope_cache": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T, T,
                                                  _P(QkNormRopeCacheConfig), T]),
+        "mi_qk_norm_rope_cache_value": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T, T, T, T,
+                                                       _P(QkNormRopeCacheConfig), T]),
         "mi_rms_norm": (ctypes.c_int, [ctypes.c_void_p, T, T, ctypes.c_float, T]),
         "mi_rope": (ctypes.c_int, [ctypes.c_void_p, T, ctypes.c_uint64, ctypes.c_float, T]),
         "mi_matmul": (ctypes.c_int, [ctypes.c_void_p, T, T, T]),
@@ -503,6 +505,16 @@ class Batch:
             self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(q_weight.desc),
             ctypes.byref(k_weight.desc), ctypes.byref(key_cache.desc), ctypes.byref(config),
             ctypes.byref(out.desc)))
+        return out
+
+    def qk_norm_rope_cache_value(self, q, k, value, q_weight, k_weight, key_cache, value_cache,
+                                 config: QkNormRopeCacheConfig, out=None) -> Tensor:
+        """qk_norm_rope_cache plus the value rows' copy_into_cache, one launch."""
+        out = self._out(q.shape, out)
+        _check(lib().mi_qk_norm_rope_cache_value(
+            self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(value.desc),
+            ctypes.byref(q_weight.desc), ctypes.byref(k_weight.desc), ctypes.byref(key_cache.desc),
+            ctypes.byref(value_cache.desc), ctypes.byref(config), ctypes.byref(out.desc)))
         return out
 
     def rms_norm(self, x: Tensor, weight: Tensor, epsilon: float, out=None) -> Tensor:

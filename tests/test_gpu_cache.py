@@ -154,3 +154,98 @@ def test_decode_loop_in_forward_layer_order(ctx):
         got_k = f16(ctx.download(key.prefix(active))).astype(np.float64)
         assert np.abs(got_k - f16(kk)).max() <= 2e-3 * max(1.0, np.abs(f16(kk)).max() / 4)
     cache.close()
+
+
+# ------------------------------------- fused Q/K transform + value append --
+
+def _fused_vs_pair(ctx, T, offset, capacity, hq=16, hkv=8, d=128):
+    q, k, v = rand(80 + T, (T, hq, d)), rand(81 + T, (T, hkv, d)), rand(82 + T, (T, hkv, d))
+    qw = (1 + 0.1 * np.random.default_rng(83).standard_normal(d)).astype(np.float16).view(np.uint16)
+    kw = (1 + 0.1 * np.random.default_rng(84).standard_normal(d)).astype(np.float16).view(np.uint16)
+    qt, kt, vt, qwt, kwt = (ctx.tensor(a) for a in (q, k, v, qw, kw))
+    cfg = mi_attn.QkNormRopeCacheConfig(offset, 1_000_000.0, 1e-6)
+    results = []
+    for fused in (False, True):
+        cache = ctx.kv_cache(1, hkv, d, capacity)
+        key, value = cache.layer(0)
+        batch = ctx.begin_batch()
+        if fused:
+            q_out = batch.qk_norm_rope_cache_value(qt, kt, vt, qwt, kwt, key, value, cfg)
+        else:
+            q_out = batch.qk_norm_rope_cache(qt, kt, qwt, kwt, key, cfg)
+            batch.copy_into_cache(vt, value, offset)
+        batch.finish()
+        results.append((ctx.download(q_out), ctx.download(key), ctx.download(value)))
+        cache.close()
+    return results, v
+
+
+@pytest.mark.parametrize("T,offset,capacity", [(1, 2047, 2048), (5, 300, 512), (3, 0, 3)])
+def test_fused_value_append_matches_the_two_calls(ctx, T, offset, capacity):
+    """mi_qk_norm_rope_cache_value == qk_norm_rope_cache then
+    copy_into_cache(value), bit for bit (qwen3.rs:704-728 order)."""
+    (pair, fused), v = _fused_vs_pair(ctx, T, offset, capacity)
+    for a, b in zip(pair, fused):
+        assert (a == b).all()
+    assert (fused[2][offset:offset + T] == v).all()
+    untouched = np.ones(capacity, bool)
+    untouched[offset:offset + T] = False
+    assert (fused[1][untouched] == 0).all() and (fused[2][untouched] == 0).all()
+
+
+def test_fused_value_append_errors(ctx):
+    hq, hkv, d = 4, 2, 64
+    cache = ctx.kv_cache(1, hkv, d, 8)
+    key, value = cache.layer(0)
+    q, k = ctx.tensor(rand(1, (2, hq, d))), ctx.tensor(rand(2, (2, hkv, d)))
+    w = ctx.tensor(rand(3, (d,)))
+    cfg = mi_attn.QkNormRopeCacheConfig(0, 1e4, 1e-6)
+    batch = ctx.begin_batch()
+    with pytest.raises(mi_attn.MiError, match="KV source/cache shapes are incompatible"):
+        batch.qk_norm_rope_cache_value(q, k, ctx.tensor(rand(4, (2, 1, d))), w, w, key, value, cfg)
+    with pytest.raises(mi_attn.MiError, match="value rows must have the key's shape"):
+        batch.qk_norm_rope_cache_value(q, k, ctx.tensor(rand(5, (1, hkv, d))), w, w, key, value, cfg)
+    with pytest.raises(mi_attn.MiError, match="KV cache capacity exceeded"):
+        small = ctx.kv_cache(1, hkv, d, 16)
+        _, small_value = small.layer(0)
+        batch.qk_norm_rope_cache_value(q, k, ctx.tensor(rand(6, (2, hkv, d))), w, w, key,
+                                       small_value.prefix(1), cfg)
+    batch.abandon()
+    small.close()
+    cache.close()
+
+
+def test_captured_fused_decode_step_replays_match_eager(ctx):
+    hq, hkv, d, cap, pos = 16, 8, 128, 1024, 600
+    cache = ctx.kv_cache(1, hkv, d, cap)
+    key, value = cache.layer(0)
+    ctx.copy_into_cache(ctx.tensor(rand(90, (pos, hkv, d))), key, 0)
+    ctx.copy_into_cache(ctx.tensor(rand(91, (pos, hkv, d))), value, 0)
+    w = ctx.tensor(rand(92, (d,), scale=0.3))
+    q_in, k_in, v_in = ctx.empty((1, hq, d)), ctx.empty((1, hkv, d)), ctx.empty((1, hkv, d))
+    cfg = mi_attn.QkNormRopeCacheConfig(pos, 1_000_000.0, 1e-6)
+    acfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
+
+    def step(batch, out=None):
+        q_rot = batch.qk_norm_rope_cache_value(q_in, k_in, v_in, w, w, key, value, cfg)
+        return batch.attention(q_rot, key.prefix(pos + 1), value.prefix(pos + 1), acfg,
+                               mi_attn.FLASH_DECODE, out=out)
+
+    o_graph = ctx.empty((1, hq, d))
+    capture = ctx.begin_capture()
+    step(capture, o_graph)
+    graph = capture.end_capture()
+    for rep in range(3):
+        ctx.upload(q_in, rand(93 + rep, (1, hq, d)))
+        ctx.upload(k_in, rand(96 + rep, (1, hkv, d)))
+        ctx.upload(v_in, rand(99 + rep, (1, hkv, d)))
+        graph.launch()
+        ctx.synchronize()
+        got = ctx.download(o_graph)
+        batch = ctx.begin_batch()
+        eager = step(batch)
+        batch.finish()
+        assert (got == ctx.download(eager)).all(), f"replay {rep}"
+        assert (ctx.download(value.prefix(pos + 1))[pos] == ctx.download(v_in)[0]).all()
+    graph.destroy()
+    cache.close()
