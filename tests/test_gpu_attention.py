@@ -180,6 +180,70 @@ def test_c4_batched_decode_seeded(ctx):
         print(f"c4 block={block}: max-abs {worst:.2e}")
 
 
+def _batched_case(ctx, seed, B, hq, hkv, d, cap, lengths):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    # head-major per sequence: [B, Hkv, cap, D] storage, [B, cap, Hkv, D] view
+    kt = ctx.tensor(np.ascontiguousarray(k.transpose(0, 2, 1, 3)))
+    vt = ctx.tensor(np.ascontiguousarray(v.transpose(0, 2, 1, 3)))
+    view = ((B, cap, hkv, d), (hkv * cap * d, d, cap * d, 1))
+    return q, k, v, kt, vt, kt.view(*view), vt.view(*view), ctx.tensor(
+        np.asarray(lengths, np.uint32), mi_attn.U32)
+
+
+def _check_batched(got, q, k, v, lengths, hq, hkv, d, cap, label):
+    for b in range(q.shape[0]):
+        n = min(int(lengths[b]), cap)
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"{label} seq {b} len {n}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 64), (32, 4, 128), (64, 4, 64)])
+def test_batched_decode_gqa_ratios_and_ragged_lengths(ctx, hq, hkv, d):
+    """The batched decode (splits merged inside the launch) for GQA 1, 2, 8
+    and 16, ragged lengths including 1 and one above the capacity (clamped),
+    several split sizes, and two launches in a row (the arrival counters must
+    be back at zero after each)."""
+    B, cap = 5, 700
+    lengths = [1, 700, 333, 64, 900]
+    q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, hq + d, B, hq, hkv, d, cap, lengths)
+    qt = ctx.tensor(q)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    for block in (0, 64, 100, 700):
+        for rep in range(2):
+            batch = ctx.begin_batch()
+            out = batch.attention_decode_batched(qt, kview, vview, lt, cfg, block)
+            batch.finish()
+            _check_batched(ctx.download(out), q, k, v, lengths, hq, hkv, d, cap,
+                           f"G={hq // hkv} d={d} block={block} rep={rep}")
+
+
+def test_batched_decode_beyond_the_arrival_counters(ctx):
+    """More (sequence, KV head) units than the context's arrival counters:
+    the split partials are merged by a second launch instead."""
+    B, hq, hkv, d, cap = 600, 8, 8, 64, 40
+    lengths = [40 - (b % 13) for b in range(B)]
+    q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, 5, B, hq, hkv, d, cap, lengths)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        out = batch.attention_decode_batched(ctx.tensor(q), kview, vview, lt, cfg, 16)
+        batch.finish()
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert names == ["attn_rows_batched", "attn_merge"]
+    got = ctx.download(out)
+    for b in range(0, B, 37):
+        n = lengths[b]
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"seq {b}")
+
+
 # --------------------------------------------------------- invariants -----
 
 def test_masked_keys_do_not_influence_output(ctx):
