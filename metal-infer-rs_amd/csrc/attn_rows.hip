@@ -103,16 +103,16 @@ __device__ __forceinline__ float dot(const Vec<VEC> &a, const Vec<VEC> &b) {
 // rescale, so the cost is one memory round trip per chunk.
 constexpr int kMergeFloats = 6144;
 
+// `base` holds nsplits consecutive partials of GC heads; the result goes to
+// out[g * o_head + d].
 template <int D, int GC, int THREADS, bool COHERENT = false>
-__device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
-                                             uint32_t nsplits, uint16_t *out,
-                                             float *buf) {
+__device__ __forceinline__ void merge_range(const float *base, uint32_t nsplits, uint16_t *out,
+                                            int64_t o_head, float *buf) {
   constexpr int ROW = D + 2;  // (max, sum, acc[D]) per split and head
   constexpr int SPLITS =
       (kMergeFloats / (GC * ROW)) > 0 ? kMergeFloats / (GC * ROW) : 1;
   constexpr int ITEMS = (GC * D + THREADS - 1) / THREADS;
   const int tid = threadIdx.x;
-  const float *base = p.partial + (size_t)unit * p.max_splits * GC * ROW;
   float M[ITEMS], L[ITEMS], A[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) M[i] = -INFINITY, L[i] = 0.0f, A[i] = 0.0f;
@@ -161,8 +161,15 @@ __device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
   for (int i = 0; i < ITEMS; ++i) {
     const int idx = tid + i * THREADS;
     if (idx >= GC * D) break;
-    out[(idx / D) * p.o_head + idx % D] = f32_to_f16(A[i] / L[i]);
+    out[(idx / D) * o_head + idx % D] = f32_to_f16(A[i] / L[i]);
   }
+}
+
+template <int D, int GC, int THREADS, bool COHERENT = false>
+__device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
+                                             uint32_t nsplits, uint16_t *out, float *buf) {
+  merge_range<D, GC, THREADS, COHERENT>(p.partial + (size_t)unit * p.max_splits * GC * (D + 2),
+                                        nsplits, out, p.o_head, buf);
 }
 
 // FUSED: with more than one split, each split publishes its partial with
@@ -410,6 +417,364 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Batched decode on MFMA with a stream-K split (one query token per sequence,
+// D = 128). Measured on MI355X at 32 sequences, L ~ U[1024, 8192], GQA 4:
+// 110 us against 126 us for the rows kernel with 768-key splits.
+//  - Work split: the launch's workgroups divide the flattened (unit, key)
+//    space of all sequences (unit = sequence, KV head, head chunk) into equal
+//    segments, so each workgroup streams the same number of bytes whatever
+//    the lengths. A segment is the tail of one unit, whole units and the head
+//    of another; each such piece ends in one partial, at slot
+//    (workgroup + unit) (unique, and a unit's pieces are consecutive slots),
+//    and the last piece of a unit to finish merges them (arrival counter).
+//  - Per 32-key tile and wave: S^T[key][head] = K Q^T on
+//    v_mfma_f32_16x16x32_f16, K rows loaded straight into the A operand
+//    (lane (g, c) holds key c, d 8 g + 32 j) and Q^T as the B operand (head
+//    c of the chunk, zero past it). Each lane then holds 8 keys of one head,
+//    so the f32 online softmax is lane-local plus a max over the four
+//    16-lane groups. O^T[d][head] += V^T P^T on the same MFMA: V rows land in
+//    the wave's LDS stage by direct loads, in a key order that matches the S
+//    accumulator, and are read transposed (ds_read_b64_tr_b16), so P is used
+//    in place.
+//  - The 4 waves take interleaved tiles, each with two register / LDS stages
+//    (the next tile is in flight while one is computed).
+constexpr int kStreamWaves = 4;
+constexpr int kStreamTile = 32;
+
+typedef __fp16 sh8_t __attribute__((ext_vector_type(8)));
+typedef float sf4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ sh8_t s_as_h8(uint4 v) { return __builtin_bit_cast(sh8_t, v); }
+__device__ __forceinline__ uint32_t s_pack_f16x2(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
+}
+__device__ __forceinline__ uint4 s_load16_stream(const uint16_t *ptr) {
+  typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+  const u4_t x = __builtin_nontemporal_load(reinterpret_cast<const u4_t *>(ptr));
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+// gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
+// at lds + 16 L (lds is wave-uniform).
+__device__ __forceinline__ void s_load_lds16(const uint16_t *global, uint16_t *lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
+}
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + b,
+// element j receives half b of the 8 bytes addressed by lane a + 4j.
+__device__ __forceinline__ uint2 s_read_tr16(const uint16_t *lds) {
+  typedef short v4s_t __attribute__((ext_vector_type(4)));
+  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (v4s_t __attribute__((address_space(3))) *)(lds));
+  return __builtin_bit_cast(uint2, v);
+}
+// Key of LDS row r of a V tile: k-slot 8 g + i of the PV operand holds key
+// 16 (i / 4) + 4 g + i % 4, the keys lane group g holds in the S accumulator.
+__device__ __forceinline__ int stream_slot_key(int r) {
+  return (((r >> 2) & 1) << 4) | (((r >> 3) & 3) << 2) | (r & 3);
+}
+// XOR applied to the 32-byte column pair of V row r: the 16 rows of one
+// transposed read then fall on 8 distinct bank groups.
+__device__ __forceinline__ int stream_swizzle(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+template <int GC>
+__global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kernel(
+    const RowsParams p) {
+  constexpr int D = 128, WAVES = kStreamWaves, KT = kStreamTile, DC = D / 32, DB = D / 16;
+  constexpr int THREADS = WAVES * 64;
+  constexpr int STAGE = KT * D;  // halves of V per wave and stage
+  static_assert(WAVES * GC * D * 4 <= WAVES * STAGE * 2, "wave merge must fit a stage");
+  static_assert(kMergeFloats * 4 <= WAVES * STAGE * 2, "split merge must fit a stage");
+  // Two V stages, one array each, so the compiler can tell the direct loads
+  // into one from the reads of the other. After the tile loop they hold the
+  // wave merge (a) and the split merge (b).
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds_a[WAVES * STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds_b[WAVES * STAGE];
+  __shared__ float s_m[WAVES][GC];
+  __shared__ float s_l[WAVES][GC];
+  __shared__ uint64_t s_pre[kStreamMaxBatch + 1];  // keys of all units before sequence b
+  __shared__ uint32_t s_last;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const uint32_t upb = p.kv_heads * p.head_chunks;  // units per sequence
+  const float c2 = p.scale_log2;
+  // Visible keys of sequence b: its cached length (one query at the end).
+  auto visible = [&](uint32_t b) -> uint32_t {
+    return p.lengths != nullptr ? min(p.lengths[b], p.kv_length) : p.kv_length;
+  };
+  // Prefix sums of the per-sequence key counts: all lengths load at once,
+  // then wave 0 scans them 64 at a time.
+  for (uint32_t b = tid; b < p.batch; b += THREADS) s_pre[b + 1] = (uint64_t)visible(b) * upb;
+  __syncthreads();
+  if (wave == 0) {
+    uint64_t carry = 0;
+    for (uint32_t c0 = 0; c0 < p.batch; c0 += 64) {
+      const uint32_t b = c0 + lane;
+      uint64_t x = b < p.batch ? s_pre[b + 1] : 0;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+      }
+      if (b < p.batch) s_pre[b + 1] = carry + x;
+      carry += __shfl(x, 63, 64);
+    }
+    if (lane == 0) s_pre[0] = 0;
+  }
+  __syncthreads();
+  // Sequences with no key: the reference divides 0 by 0.
+  for (uint32_t b = blockIdx.x; b < p.batch; b += gridDim.x)
+    if (s_pre[b + 1] == s_pre[b])
+      for (uint32_t idx = tid; idx < p.q_heads * D; idx += THREADS)
+        p.out[(int64_t)b * p.o_seq + (int64_t)(idx / D) * p.o_head + idx % D] = 0x7e00;
+  const uint64_t total = s_pre[p.batch];
+  // At least kStreamMinKeys per workgroup; the rest of the grid idles.
+  const uint64_t W = min((uint64_t)gridDim.x, max((uint64_t)1, total / kStreamMinKeys));
+  const uint64_t seg = (total + W - 1) / W;
+  const uint32_t w = blockIdx.x;
+  uint64_t pos = (uint64_t)w * seg;
+  const uint64_t end = min(pos + seg, total);
+  if (pos >= end) return;
+  // The sequence holding key `at`: the last b with s_pre[b] <= at (which
+  // skips sequences without keys).
+  auto find_seq = [&](uint64_t at) -> uint32_t {
+    uint32_t lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) / 2;
+      if (s_pre[mid] <= at) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+  uint32_t b = find_seq(pos);
+
+  // Loop-invariant byte offsets inside a full tile (its base is uniform).
+  // K: lane (grp, col) loads key col (+16 for the second half), d 8 grp +
+  // 32 j. V: direct-load instruction i writes LDS rows 4i .. 4i + 3, lane L
+  // row 4i + L / 16 and physical 16-byte chunk L % 16.
+  uint32_t v_off[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4), pc = lane & 15;
+    const int chunk = 2 * ((pc >> 1) ^ stream_swizzle(r)) + (pc & 1);
+    v_off[i] = (uint32_t)(stream_slot_key(r) * p.v_pos + chunk * 8) * 2u;
+  }
+  uint32_t k_off[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) k_off[hf] = (uint32_t)((16 * hf + col) * p.k_pos + 8 * grp) * 2u;
+  // Transposed V reads: lane (grp, mu) addresses row 8 grp + mu / 4 (and
+  // + 4), d 16 dt + 4 (mu % 4).
+  const int mu = lane & 15;
+  const int tr_row = 8 * grp + (mu >> 2);
+  const int tr_base = tr_row * D + 4 * (mu & 1);
+  const int tr_hi = (mu & 3) >> 1;
+  const int tr_f = stream_swizzle(tr_row);
+
+  while (pos < end) {
+    const uint32_t len_b = visible(b);
+    const uint64_t rel = pos - s_pre[b];
+    const uint32_t j = (uint32_t)(rel / len_b);  // unit within the sequence
+    const uint32_t k0 = (uint32_t)(rel % len_b);
+    const uint32_t k1 = (uint32_t)min((uint64_t)len_b, k0 + (end - pos));
+    const uint32_t kvh = j / p.head_chunks, hc = j % p.head_chunks;
+    const uint32_t unit = b * upb + j;
+    const uint64_t unit_start = s_pre[b] + (uint64_t)j * len_b;
+    const uint32_t first_wg = (uint32_t)(unit_start / seg);
+    const uint32_t last_wg = (uint32_t)((unit_start + len_b - 1) / seg);
+    const uint32_t h0 = kvh * p.group + hc * GC;
+    uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)h0 * p.o_head;
+    const uint32_t ntiles = (k1 - k0 + KT - 1) / KT;
+
+    sh8_t qop[DC];
+    {
+      const uint16_t *qb = p.q + (int64_t)b * p.q_seq + (int64_t)(h0 + min(col, GC - 1)) * p.q_head + 8 * grp;
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        qop[c] = col < GC ? s_as_h8(*reinterpret_cast<const uint4 *>(qb + 32 * c))
+                          : s_as_h8(make_uint4(0, 0, 0, 0));
+    }
+    const uint16_t *kb = p.k + (int64_t)b * p.k_seq + (int64_t)kvh * p.k_head;
+    const uint16_t *vb = p.v + (int64_t)b * p.v_seq + (int64_t)kvh * p.v_head;
+    sf4_t o[DB];
+#pragma unroll
+    for (int dt = 0; dt < DB; ++dt) o[dt] = sf4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;  // raw-score reference max, row sum
+
+    auto issue = [&](uint32_t ti, uint4 *kr, uint16_t *vst) __attribute__((always_inline)) {
+      const uint32_t base = k0 + ti * KT;
+      uint16_t *vdst = vst + wave * STAGE;
+      if (base + KT <= k1) {
+        const char *kt = reinterpret_cast<const char *>(kb + (int64_t)base * p.k_pos);
+        const char *vt = reinterpret_cast<const char *>(vb + (int64_t)base * p.v_pos);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int c = 0; c < DC; ++c)
+            kr[hf * DC + c] = s_load16_stream(reinterpret_cast<const uint16_t *>(kt + k_off[hf] + 64 * c));
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          s_load_lds16(reinterpret_cast<const uint16_t *>(vt + v_off[i]), vdst + i * 512);
+      } else {
+        // The piece's last, partial tile: rows past it re-read its last key
+        // (always in bounds) and are masked.
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint32_t key = min(base + 16 * hf + col, k1 - 1);
+#pragma unroll
+          for (int c = 0; c < DC; ++c)
+            kr[hf * DC + c] = s_load16_stream(kb + (int64_t)key * p.k_pos + 8 * grp + 32 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = 4 * i + (lane >> 4), pc = lane & 15;
+          const int chunk = 2 * ((pc >> 1) ^ stream_swizzle(r)) + (pc & 1);
+          const uint32_t key = min(base + (uint32_t)stream_slot_key(r), k1 - 1);
+          s_load_lds16(vb + (int64_t)key * p.v_pos + chunk * 8, vdst + i * 512);
+        }
+      }
+    };
+    auto compute = [&](uint32_t ti, const uint4 *kr, const uint16_t *vst) __attribute__((always_inline)) {
+      const uint32_t base = k0 + ti * KT;
+      sf4_t s[2];  // s[hf][e]: head col, key 16 hf + 4 grp + e
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        s[hf] = sf4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+          s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s_as_h8(kr[hf * DC + c]), qop[c], s[hf], 0, 0, 0);
+      }
+      if (base + KT > k1) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (base + 16 * hf + 4 * grp + e >= k1) s[hf][e] = -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Lazy rescale: the reference max moves only when some head outgrows
+      // it by 2^8 (always on a piece's first tile), which keeps P <= 256.
+      if (__any((mx - m_run) * c2 > 8.0f)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.0f : exp2_raw((m_run - m_new) * c2);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DB; ++dt) o[dt] *= alpha;
+        m_run = m_new;
+      }
+      const float mc = m_run == -INFINITY ? 0.0f : m_run * c2;
+      uint32_t pw[4];  // P as f16 pairs in the PV operand's key order
+      float ps = 0.0f;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const uint32_t wv = s_pack_f16x2(exp2_raw(fmaf(s[hf][e], c2, -mc)),
+                                           exp2_raw(fmaf(s[hf][e + 1], c2, -mc)));
+          pw[2 * hf + e / 2] = wv;
+          // The row sum uses the same f16-rounded weights as P V.
+          ps = dot2(wv, 0x3c003c00u, ps);
+        }
+      l_run += ps;
+      const sh8_t pb = s_as_h8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+      const uint16_t *vw = vst + wave * STAGE;
+#pragma unroll
+      for (int dt = 0; dt < DB; ++dt) {
+        const uint16_t *a0 = vw + tr_base + (2 * (dt ^ tr_f) + tr_hi) * 8;
+        const uint2 lo = s_read_tr16(a0), hi = s_read_tr16(a0 + 4 * D);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s_as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
+                                                       o[dt], 0, 0, 0);
+      }
+    };
+
+    // Wave w takes tiles w, w + 4, ...; the register and LDS stages
+    // alternate (loop unrolled by two so each is a compile-time choice).
+    uint4 kra[2 * DC], krb[2 * DC];
+    uint32_t ti = wave;
+    if (ti < ntiles) issue(ti, kra, v_lds_a);
+    while (ti < ntiles) {
+      uint32_t nx = ti + WAVES;
+      if (nx < ntiles) issue(nx, krb, v_lds_b);
+      compute(ti, kra, v_lds_a);
+      ti = nx;
+      if (ti >= ntiles) break;
+      nx = ti + WAVES;
+      if (nx < ntiles) issue(nx, kra, v_lds_a);
+      compute(ti, krb, v_lds_b);
+      ti = nx;
+    }
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    // Merge the waves through LDS, then write the unit's output (a piece
+    // that is the whole unit) or this piece's partial.
+    __syncthreads();
+    float *s_o = reinterpret_cast<float *>(v_lds_a);  // [WAVES][GC][D]
+    if (col < GC) {
+      if (grp == 0) {
+        s_m[wave][col] = m_run;
+        s_l[wave][col] = l_run;
+      }
+#pragma unroll
+      for (int dt = 0; dt < DB; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_o[(wave * GC + col) * D + 16 * dt + 4 * grp + e] = o[dt][e];
+    }
+    __syncthreads();
+    const bool direct = first_wg == last_wg;
+    float *part = p.partial + (size_t)(w + unit) * GC * (D + 2);
+    for (int idx = tid; idx < GC * D; idx += THREADS) {
+      const int g = idx / D, d = idx % D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) M = fmaxf(M, s_m[wv][g]);
+      float L = 0.0f, A = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) {
+        const float f = s_m[wv][g] == -INFINITY ? 0.0f : exp2_raw((s_m[wv][g] - M) * c2);
+        L += s_l[wv][g] * f;
+        A += s_o[(wv * GC + g) * D + d] * f;
+      }
+      if (direct) {
+        out[g * p.o_head + d] = f32_to_f16(A / L);
+      } else {
+        // Partials keep the max in log2-scaled units, as the rows kernel's.
+        store_coherent(part + g * (D + 2) + 2 + d, A);
+        if (d == 0) {
+          store_coherent(part + g * (D + 2), M == -INFINITY ? -INFINITY : M * c2);
+          store_coherent(part + g * (D + 2) + 1, L);
+        }
+      }
+    }
+    if (!direct) {
+      // Every store of this workgroup has completed before the arrival
+      // counts; the unit's last piece merges all of them.
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      const uint32_t pieces = last_wg - first_wg + 1;
+      if (tid == 0) {
+        const uint32_t arrived = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = arrived == pieces - 1;
+        if (last) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last != 0)
+        merge_range<D, GC, THREADS, true>(p.partial + (size_t)(first_wg + unit) * GC * (D + 2),
+                                          pieces, out, p.o_head, reinterpret_cast<float *>(v_lds_b));
+    }
+    // The next piece's loads overwrite both stages.
+    __syncthreads();
+    pos += k1 - k0;
+    if (pos < end && pos >= s_pre[b + 1]) b = find_seq(pos);
+  }
+}
+
 // Merges the split partials of one (row, KV head, head chunk) unit: the
 // log-sum-exp combine of the reference's reduce kernels
 // (transformer.metal:2251-2316). Launched after attn_rows_kernel on the same
@@ -474,7 +839,29 @@ hipError_t launch_rows_d(const RowsParams &p, uint32_t waves, uint32_t chunk,
   return hipErrorInvalidValue;
 }
 
+template <int GC>
+hipError_t launch_stream_gc(const RowsParams &p, uint32_t workgroups, const Launch &l) {
+  return dispatch(attn_decode_stream_kernel<GC>, dim3(workgroups), dim3(kStreamWaves * 64), 0, l, p);
+}
+
 }  // namespace
+
+uint32_t stream_chunk(uint32_t group) {
+  for (uint32_t c : {16u, 8u, 4u, 2u}) if (group % c == 0) return c;
+  return 1;
+}
+
+hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, uint32_t workgroups,
+                                const Launch &l) {
+  switch (chunk) {
+    case 16: return launch_stream_gc<16>(p, workgroups, l);
+    case 8: return launch_stream_gc<8>(p, workgroups, l);
+    case 4: return launch_stream_gc<4>(p, workgroups, l);
+    case 2: return launch_stream_gc<2>(p, workgroups, l);
+    case 1: return launch_stream_gc<1>(p, workgroups, l);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 uint32_t rows_chunk(uint32_t group) {
   for (uint32_t c : {8u, 4u, 2u}) if (group % c == 0) return c;

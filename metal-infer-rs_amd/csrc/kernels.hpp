@@ -152,6 +152,21 @@ hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
 // Largest head chunk (of 8, 4, 2, 1) that divides `group`.
 uint32_t rows_chunk(uint32_t group);
 
+// Batched decode (one query token per sequence, head_dim 128) on MFMA with
+// a stream-K split: `workgroups` workgroups share the keys of all sequences
+// equally (each at least kStreamMinKeys). RowsParams as for the rows kernel
+// with tokens = 1, head_chunks = group / chunk and per-sequence `lengths`
+// (required); `partial` holds
+// (workgroups + units) * chunk * (D + 2) floats and `counters` one zeroed
+// counter per unit. batch <= kStreamMaxBatch; a full 32-key tile of K or V
+// must span less than 4 GiB (32 * pos stride * 2 bytes).
+constexpr uint32_t kStreamMaxBatch = 1024;
+constexpr uint32_t kStreamMinKeys = 512;
+hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, uint32_t workgroups,
+                                const Launch &l);
+// Head chunk of the stream kernel: the largest of 16, 8, 4, 2, 1 dividing `group`.
+uint32_t stream_chunk(uint32_t group);
+
 // Runs rows [row_begin, row_begin + row_count) of the flattened
 // (token, head) grid. Scores of up to kNaiveLdsKeys keys live in LDS; longer
 // rows spill to NaiveParams::scores, which must hold row_count * L floats.

@@ -528,6 +528,44 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   p.T = 1;
   p.Hq = config->query_heads, p.Hkv = config->kv_heads, p.D = config->head_dim;
   p.G = p.Hq / p.Hkv;
+  // Default: the stream-K MFMA kernel (head_dim 128), which gives every
+  // workgroup the same share of all sequences' keys. Explicit split sizes
+  // keep the rows kernel.
+  if (block_keys == 0 && p.D == 128 && (uint64_t)B <= kernels::kStreamMaxBatch &&
+      32 * (uint64_t)std::max(k->stride[1], v->stride[1]) * 2 < (1ull << 32) &&
+      q->stride[2] == 1 && k->stride[3] == 1 && v->stride[3] == 1) {
+    const uint32_t chunk = kernels::stream_chunk(p.G);
+    const uint64_t units = (uint64_t)B * p.Hkv * (p.G / chunk);
+    const uint32_t cus = std::max<uint32_t>(batch->ctx->compute_units, 1);
+    const uint32_t workgroups = 2 * cus;
+    if (units <= batch->ctx->split_counter_count && (uint64_t)p.Hkv * (p.G / chunk) <= 0xffffu) {
+      kernels::RowsParams rp{};
+      rp.q = static_cast<const uint16_t *>(q->data);
+      rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
+      rp.k = static_cast<const uint16_t *>(k->data);
+      rp.k_seq = k->stride[0], rp.k_pos = k->stride[1], rp.k_head = k->stride[2];
+      rp.v = static_cast<const uint16_t *>(v->data);
+      rp.v_seq = v->stride[0], rp.v_pos = v->stride[1], rp.v_head = v->stride[2];
+      rp.out = static_cast<uint16_t *>(out->data);
+      rp.o_seq = out->stride[0], rp.o_tok = 0, rp.o_head = out->stride[1];
+      rp.lengths = static_cast<const uint32_t *>(lengths->data);
+      rp.batch = (uint32_t)B, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+      rp.group = p.G, rp.head_chunks = p.G / chunk;
+      rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
+      rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
+      const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
+      void *scratch = nullptr;
+      if ((st = scratch_alloc(batch, bytes, &scratch)) != MI_OK) return st;
+      rp.partial = static_cast<float *>(scratch);
+      rp.counters = batch->ctx->split_counters;
+      st = launch(batch, "attn_decode_stream", [&](const kernels::Launch &s) {
+        return kernels::launch_decode_stream(rp, chunk, workgroups, s);
+      });
+      // In-order execution makes the range reusable by later work of the batch.
+      scratch_free(batch->ctx, scratch);
+      return st;
+    }
+  }
   // 768-key splits (measured at B=32, L ~ U[1024, 8192], whole call: 768 ->
   // 4.7 TB/s; 640-960 -> 4.5-4.7; every power of two 512-4096 -> 3.8-4.1).
   // Power-of-two splits start every workgroup at the same offset modulo a

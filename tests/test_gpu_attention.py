@@ -168,9 +168,17 @@ def test_c4_batched_decode_seeded(ctx):
     lengths = ctx.tensor(c.lengths, mi_attn.U32)
     cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
     for block in (0, 256, 1024):
-        batch = ctx.begin_batch()
-        out = batch.attention_decode_batched(qt, kview, vview, lengths, cfg, block)
-        batch.finish()
+        ctx.take_kernel_profiles()
+        ctx.set_kernel_profiling(True)
+        try:
+            batch = ctx.begin_batch()
+            out = batch.attention_decode_batched(qt, kview, vview, lengths, cfg, block)
+            batch.finish()
+            names = [name for name, _ in ctx.take_kernel_profiles()]
+        finally:
+            ctx.set_kernel_profiling(False)
+        # Default: stream-K MFMA kernel; explicit split sizes: rows kernel.
+        assert names == (["attn_decode_stream"] if block == 0 else ["attn_rows_batched"]), names
         got = ctx.download(out)
         worst = 0.0
         for b in range(B):
@@ -218,6 +226,75 @@ def test_batched_decode_gqa_ratios_and_ragged_lengths(ctx, hq, hkv, d):
             batch.finish()
             _check_batched(ctx.download(out), q, k, v, lengths, hq, hkv, d, cap,
                            f"G={hq // hkv} d={d} block={block} rep={rep}")
+
+
+@pytest.mark.parametrize("B,hq,hkv,cap,lengths", [
+    # GQA 16 (one 16-head chunk), GQA 32 (two chunks), GQA 3 and 12 (chunks
+    # of 1 and 4), with zero-length sequences between others.
+    (6, 32, 2, 300, [300, 0, 17, 0, 299, 1]),
+    (3, 64, 2, 520, [520, 7, 519]),
+    (4, 12, 4, 260, [0, 260, 33, 129]),
+    (5, 48, 4, 140, [140, 1, 70, 0, 139]),
+    # One long sequence: every unit is split over many workgroups, so the
+    # last piece merges dozens of partials (several merge rounds).
+    (1, 16, 8, 20000, [20000]),
+    # Many short sequences: one workgroup's segment covers many units.
+    (1024, 8, 2, 24, [(b * 7) % 25 for b in range(1024)]),
+])
+def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
+    """The default batched decode at head_dim 128 runs the stream-K MFMA
+    kernel: workgroups take equal shares of all sequences' keys, pieces of a
+    unit are merged by its last piece. Checked against the oracle for every
+    sequence (a zero-length one gives NaN, as the reference's 0/0), twice in
+    a row (arrival counters back at zero)."""
+    d = 128
+    q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, B + hq + cap, B, hq, hkv, d, cap, lengths)
+    qt = ctx.tensor(q)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    for rep in range(2):
+        ctx.take_kernel_profiles()
+        ctx.set_kernel_profiling(True)
+        try:
+            batch = ctx.begin_batch()
+            out = batch.attention_decode_batched(qt, kview, vview, lt, cfg, 0)
+            batch.finish()
+            names = [name for name, _ in ctx.take_kernel_profiles()]
+        finally:
+            ctx.set_kernel_profiling(False)
+        assert names == ["attn_decode_stream"], names
+        got = ctx.download(out)
+        for b in range(B):
+            n = min(int(lengths[b]), cap)
+            if B > 64 and b % 41 != 0 and n != 0:
+                continue
+            if n == 0:
+                assert np.isnan(got[b].view(np.float16).astype(np.float32)).all(), f"seq {b}"
+                continue
+            ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+            assert_parity(got[b:b + 1], ref, label=f"B={B} G={hq // hkv} seq {b} len {n} rep {rep}")
+
+
+def test_batched_decode_beyond_the_stream_batch_limit(ctx):
+    """Past the stream kernel's batch limit the rows kernel serves the call."""
+    B, hq, hkv, d, cap = 1025, 8, 8, 128, 8
+    lengths = [1 + b % 8 for b in range(B)]
+    q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, 9, B, hq, hkv, d, cap, lengths)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        out = batch.attention_decode_batched(ctx.tensor(q), kview, vview, lt, cfg, 0)
+        batch.finish()
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert names == ["attn_rows_batched"], names
+    got = ctx.download(out)
+    for b in range(0, B, 97):
+        n = lengths[b]
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"seq {b}")
 
 
 def test_batched_decode_beyond_the_arrival_counters(ctx):
