@@ -26,7 +26,7 @@ sys.path.insert(0, str(Path(__file__).resolve().parent))
 # Library launch record -> rocprof kernel of each workload's dominant kernel.
 DOMINANT = {
     "c2": ("attn_rows", "attn_rows_kernel"),
-    "c4": ("attn_rows_batched", "attn_rows_kernel"),
+    "c4": ("attn_decode_stream", "attn_decode_stream_kernel"),
     "c3": ("attn_prefill", "attn_prefill_kernel"),
     "c5": ("attn_prefill", "attn_prefill_kernel"),
 }

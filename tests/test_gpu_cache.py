@@ -168,6 +168,10 @@ def _fused_vs_pair(ctx, T, offset, capacity, hq=16, hkv=8, d=128):
     for fused in (False, True):
         cache = ctx.kv_cache(1, hkv, d, capacity)
         key, value = cache.layer(0)
+        # The cache starts uninitialised (like the reference's context.empty):
+        # a sentinel shows which rows each path writes.
+        ctx.upload(key, np.full((capacity, hkv, d), 0x7bff, dtype=np.uint16))
+        ctx.upload(value, np.full((capacity, hkv, d), 0x7bfe, dtype=np.uint16))
         batch = ctx.begin_batch()
         if fused:
             q_out = batch.qk_norm_rope_cache_value(qt, kt, vt, qwt, kwt, key, value, cfg)
@@ -190,7 +194,7 @@ def test_fused_value_append_matches_the_two_calls(ctx, T, offset, capacity):
     assert (fused[2][offset:offset + T] == v).all()
     untouched = np.ones(capacity, bool)
     untouched[offset:offset + T] = False
-    assert (fused[1][untouched] == 0).all() and (fused[2][untouched] == 0).all()
+    assert (fused[1][untouched] == 0x7bff).all() and (fused[2][untouched] == 0x7bfe).all()
 
 
 def test_fused_value_append_errors(ctx):
