@@ -119,10 +119,6 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
   const uint32_t G = p.group;
-  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
-  // by linear id, so id % 8 selects the XCD. When the KV heads split evenly
-  // over the XCDs, each XCD gets whole heads (their K/V stay in its L2);
-  // within an XCD the heaviest row tiles go first.
   // Dispatch order: workgroups are handed out in linear-id order, and
   // round-robin over the 8 XCDs, so id % 8 selects the XCD. When the KV
   // heads split evenly over the XCDs, each XCD gets whole heads (their K/V

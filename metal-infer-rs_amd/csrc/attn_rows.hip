@@ -13,10 +13,13 @@
 //  - per-row dot products reduce with DPP inside a 16-lane row;
 //  - scores and the softmax stay in f32 (v_exp_f32 on log2-scaled scores);
 //  - with more than one split, each split writes a (max, sum, acc[D])
-//    partial and attn_merge_kernel combines them. Publishing partials inside
-//    one kernel needs an agent-scope release per workgroup, which on a
-//    multi-XCD part writes back the XCD's whole L2; measured slower than the
-//    second launch for every split size, so the kernel boundary does it.
+//    partial. Either the unit's last split merges them in the same launch
+//    (device-scope partial stores, a wait for their completion, then an
+//    arrival counter: no cache-wide release fence, which on a multi-XCD part
+//    writes back the XCD's whole L2 and measured slower than a second
+//    launch), or attn_merge_kernel does in a second launch.
+// The batched decode at head_dim 128 has its own kernel further down
+// (attn_decode_stream_kernel: MFMA tiles, stream-K split).
 #include <type_traits>
 
 #include "device_common.hpp"

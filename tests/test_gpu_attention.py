@@ -274,6 +274,38 @@ def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
             assert_parity(got[b:b + 1], ref, label=f"B={B} G={hq // hkv} seq {b} len {n} rep {rep}")
 
 
+def test_batched_decode_stream_k_token_major_cache(ctx):
+    """The stream-K kernel on a token-major cache ([B, C, Hkv, D] contiguous,
+    so a key row's stride is Hkv * D rather than D)."""
+    B, hq, hkv, d, cap = 4, 32, 8, 128, 1000
+    lengths = [1000, 3, 517, 0]
+    rng = np.random.default_rng(77)
+    q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    kt, vt = ctx.tensor(k), ctx.tensor(v)
+    lt = ctx.tensor(np.asarray(lengths, np.uint32), mi_attn.U32)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        out = batch.attention_decode_batched(ctx.tensor(q), kt, vt, lt, cfg, 0)
+        batch.finish()
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert names == ["attn_decode_stream"], names
+    got = ctx.download(out)
+    for b in range(B):
+        n = lengths[b]
+        if n == 0:
+            assert np.isnan(got[b].view(np.float16).astype(np.float32)).all()
+            continue
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"token-major seq {b} len {n}")
+
+
 def test_batched_decode_beyond_the_stream_batch_limit(ctx):
     """Past the stream kernel's batch limit the rows kernel serves the call."""
     B, hq, hkv, d, cap = 1025, 8, 8, 128, 8
