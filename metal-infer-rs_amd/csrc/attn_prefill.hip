@@ -30,8 +30,6 @@ constexpr int BM = kPrefillBlockM;  // packed rows per workgroup
 constexpr int BN = kPrefillBlockN;  // keys per KV tile
 constexpr int THREADS = 256;        // 4 waves x 32 rows
 
-typedef __fp16 h8_t __attribute__((ext_vector_type(8)));
-
 // Column of key `key` (0..63 within a tile) in the transposed V tile: bits
 // 2 and 3 swapped, which is the key order of the P operand (see above).
 __device__ __forceinline__ int vt_col(int key) {
@@ -42,10 +40,6 @@ __device__ __forceinline__ uint4 load16(const uint16_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
 
-__device__ __forceinline__ h8_t as_h8(uint4 v) {
-  return __builtin_bit_cast(h8_t, v);
-}
-
 // Packs the f16 halves of words a and b: lo -> (a.lo, b.lo), hi -> (a.hi, b.hi).
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x05040100u);
@@ -54,25 +48,6 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-// v_cvt_pk_f16_f32: two f32 -> packed f16, round to nearest even.
-__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  typedef float f2_t __attribute__((ext_vector_type(2)));
-  const f2_t v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
-}
-
-// gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
-// at lds + 16 L (lds is wave-uniform).
-__device__ __forceinline__ void load_lds16(const uint16_t *global, uint16_t *lds) {
-  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
-}
-// gfx950 ds_read_b64_tr_b16: 4 halves, transposed across each 16-lane group.
-__device__ __forceinline__ uint2 read_tr16(const uint16_t *lds) {
-  typedef short v4s_t __attribute__((ext_vector_type(4)));
-  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (v4s_t __attribute__((address_space(3))) *)(lds));
-  return __builtin_bit_cast(uint2, v);
-}
 
 
 // O and l are rescaled only when a row's max grows past its reference by

@@ -446,32 +446,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
 constexpr int kStreamWaves = 4;
 constexpr int kStreamTile = 32;
 
-typedef __fp16 sh8_t __attribute__((ext_vector_type(8)));
 typedef float sf4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ sh8_t s_as_h8(uint4 v) { return __builtin_bit_cast(sh8_t, v); }
-__device__ __forceinline__ uint32_t s_pack_f16x2(float lo, float hi) {
-  typedef float f2_t __attribute__((ext_vector_type(2)));
-  const f2_t v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
-}
-__device__ __forceinline__ uint4 s_load16_stream(const uint16_t *ptr) {
+__device__ __forceinline__ uint4 load16_stream(const uint16_t *ptr) {
   typedef unsigned u4_t __attribute__((ext_vector_type(4)));
   const u4_t x = __builtin_nontemporal_load(reinterpret_cast<const u4_t *>(ptr));
   return make_uint4(x.x, x.y, x.z, x.w);
-}
-// gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
-// at lds + 16 L (lds is wave-uniform).
-__device__ __forceinline__ void s_load_lds16(const uint16_t *global, uint16_t *lds) {
-  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
-}
-// gfx950 ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + b,
-// element j receives half b of the 8 bytes addressed by lane a + 4j.
-__device__ __forceinline__ uint2 s_read_tr16(const uint16_t *lds) {
-  typedef short v4s_t __attribute__((ext_vector_type(4)));
-  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (v4s_t __attribute__((address_space(3))) *)(lds));
-  return __builtin_bit_cast(uint2, v);
 }
 // Key of LDS row r of a V tile: k-slot 8 g + i of the PV operand holds key
 // 16 (i / 4) + 4 g + i % 4, the keys lane group g holds in the S accumulator.
@@ -590,13 +570,13 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
     uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)h0 * p.o_head;
     const uint32_t ntiles = (k1 - k0 + KT - 1) / KT;
 
-    sh8_t qop[DC];
+    h8_t qop[DC];
     {
       const uint16_t *qb = p.q + (int64_t)b * p.q_seq + (int64_t)(h0 + min(col, GC - 1)) * p.q_head + 8 * grp;
 #pragma unroll
       for (int c = 0; c < DC; ++c)
-        qop[c] = col < GC ? s_as_h8(*reinterpret_cast<const uint4 *>(qb + 32 * c))
-                          : s_as_h8(make_uint4(0, 0, 0, 0));
+        qop[c] = col < GC ? as_h8(*reinterpret_cast<const uint4 *>(qb + 32 * c))
+                          : as_h8(make_uint4(0, 0, 0, 0));
     }
     const uint16_t *kb = p.k + (int64_t)b * p.k_seq + (int64_t)kvh * p.k_head;
     const uint16_t *vb = p.v + (int64_t)b * p.v_seq + (int64_t)kvh * p.v_head;
@@ -615,10 +595,10 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int c = 0; c < DC; ++c)
-            kr[hf * DC + c] = s_load16_stream(reinterpret_cast<const uint16_t *>(kt + k_off[hf] + 64 * c));
+            kr[hf * DC + c] = load16_stream(reinterpret_cast<const uint16_t *>(kt + k_off[hf] + 64 * c));
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          s_load_lds16(reinterpret_cast<const uint16_t *>(vt + v_off[i]), vdst + i * 512);
+          load_lds16(reinterpret_cast<const uint16_t *>(vt + v_off[i]), vdst + i * 512);
       } else {
         // The piece's last, partial tile: rows past it re-read its last key
         // (always in bounds) and are masked.
@@ -627,14 +607,14 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
           const uint32_t key = min(base + 16 * hf + col, k1 - 1);
 #pragma unroll
           for (int c = 0; c < DC; ++c)
-            kr[hf * DC + c] = s_load16_stream(kb + (int64_t)key * p.k_pos + 8 * grp + 32 * c);
+            kr[hf * DC + c] = load16_stream(kb + (int64_t)key * p.k_pos + 8 * grp + 32 * c);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int r = 4 * i + (lane >> 4), pc = lane & 15;
           const int chunk = 2 * ((pc >> 1) ^ stream_swizzle(r)) + (pc & 1);
           const uint32_t key = min(base + (uint32_t)stream_slot_key(r), k1 - 1);
-          s_load_lds16(vb + (int64_t)key * p.v_pos + chunk * 8, vdst + i * 512);
+          load_lds16(vb + (int64_t)key * p.v_pos + chunk * 8, vdst + i * 512);
         }
       }
     };
@@ -646,7 +626,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
         s[hf] = sf4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < DC; ++c)
-          s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s_as_h8(kr[hf * DC + c]), qop[c], s[hf], 0, 0, 0);
+          s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kr[hf * DC + c]), qop[c], s[hf], 0, 0, 0);
       }
       if (base + KT > k1) {
 #pragma unroll
@@ -676,20 +656,20 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int e = 0; e < 4; e += 2) {
-          const uint32_t wv = s_pack_f16x2(exp2_raw(fmaf(s[hf][e], c2, -mc)),
+          const uint32_t wv = pack_f16x2(exp2_raw(fmaf(s[hf][e], c2, -mc)),
                                            exp2_raw(fmaf(s[hf][e + 1], c2, -mc)));
           pw[2 * hf + e / 2] = wv;
           // The row sum uses the same f16-rounded weights as P V.
           ps = dot2(wv, 0x3c003c00u, ps);
         }
       l_run += ps;
-      const sh8_t pb = s_as_h8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
+      const h8_t pb = as_h8(make_uint4(pw[0], pw[1], pw[2], pw[3]));
       const uint16_t *vw = vst + wave * STAGE;
 #pragma unroll
       for (int dt = 0; dt < DB; ++dt) {
         const uint16_t *a0 = vw + tr_base + (2 * (dt ^ tr_f) + tr_hi) * 8;
-        const uint2 lo = s_read_tr16(a0), hi = s_read_tr16(a0 + 4 * D);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(s_as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
+        const uint2 lo = read_tr16(a0), hi = read_tr16(a0 + 4 * D);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb,
                                                        o[dt], 0, 0, 0);
       }
     };

@@ -1,5 +1,6 @@
 // Device helpers for the CDNA4 (gfx950) kernels: f16 vectors, DPP row
-// reductions and the raw exp2 instruction.
+// reductions, the raw exp2 instruction, MFMA operand packing and the gfx950
+// direct-to-LDS and transposed LDS accesses.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -83,6 +84,32 @@ __device__ __forceinline__ float lane_group_sum(float x) {
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(fp16x2_t, a),
                                 __builtin_bit_cast(fp16x2_t, b), c, false);
+}
+
+// Eight f16 values of one MFMA operand register quad.
+typedef __fp16 h8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ h8_t as_h8(uint4 v) { return __builtin_bit_cast(h8_t, v); }
+
+// v_cvt_pk_f16_f32: two f32 -> packed f16, round to nearest even.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, half2_t));
+}
+
+// gfx950 direct global->LDS load of 16 bytes per lane: lane L's bytes land
+// at lds + 16 L (lds is wave-uniform).
+__device__ __forceinline__ void load_lds16(const uint16_t *global, uint16_t *lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
+}
+
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + b,
+// element j receives half b of the 8 bytes addressed by lane a + 4j.
+__device__ __forceinline__ uint2 read_tr16(const uint16_t *lds) {
+  typedef short v4s_t __attribute__((ext_vector_type(4)));
+  const v4s_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (v4s_t __attribute__((address_space(3))) *)(lds));
+  return __builtin_bit_cast(uint2, v);
 }
 
 __device__ __forceinline__ float lo_f16(uint32_t packed) {
