@@ -272,12 +272,15 @@ mi_status mi_attention_plan(const mi_context *ctx, const mi_tensor *q,
                             mi_attention_plan_info *info);
 
 /* Batched split-K decode: B sequences, one new query each. No counterpart
- * in the reference (its decode is single-sequence); it runs the same kernel
- * over a flat (sequence, KV head, split) grid. q [B, Hq, D]; k/v
+ * in the reference (its decode is single-sequence). q [B, Hq, D]; k/v
  * [B, C, Hkv, D] views (C = per-sequence capacity); lengths: device u32 [B]
- * with 1 <= lengths[b] <= C (values above C are clamped to C); causal over
- * each sequence (query at position lengths[b] - 1). out [B, Hq, D].
- * config->query_offset is ignored. block_keys = 0 picks a default. */
+ * (values above C are clamped to C; a sequence of length 0 gets NaN, the
+ * reference's 0/0); causal over each sequence (query at position
+ * lengths[b] - 1). out [B, Hq, D]. config->query_offset is ignored.
+ * block_keys = 0 picks the default: at head_dim 128 and B <= 1024 an MFMA
+ * kernel whose workgroups share all sequences' keys equally (stream-K),
+ * otherwise the rows kernel over a flat (sequence, KV head, split) grid.
+ * block_keys > 0 runs the rows kernel with splits of that many keys. */
 mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q,
                                       const mi_tensor *k, const mi_tensor *v,
                                       const mi_tensor *lengths,
