@@ -528,31 +528,30 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   p.T = 1;
   p.Hq = config->query_heads, p.Hkv = config->kv_heads, p.D = config->head_dim;
   p.G = p.Hq / p.Hkv;
+  // Tensor views and per-sequence lengths, shared by both kernels.
+  kernels::RowsParams rp{};
+  rp.q = static_cast<const uint16_t *>(q->data);
+  rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
+  rp.k = static_cast<const uint16_t *>(k->data);
+  rp.k_seq = k->stride[0], rp.k_pos = k->stride[1], rp.k_head = k->stride[2];
+  rp.v = static_cast<const uint16_t *>(v->data);
+  rp.v_seq = v->stride[0], rp.v_pos = v->stride[1], rp.v_head = v->stride[2];
+  rp.out = static_cast<uint16_t *>(out->data);
+  rp.o_seq = out->stride[0], rp.o_tok = 0, rp.o_head = out->stride[1];
+  rp.lengths = static_cast<const uint32_t *>(lengths->data);
+  rp.batch = (uint32_t)B, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+  rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
+  rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
   // Default: the stream-K MFMA kernel (head_dim 128), which gives every
-  // workgroup the same share of all sequences' keys. Explicit split sizes
-  // keep the rows kernel.
+  // workgroup the same share of all sequences' keys (2 per CU). Explicit
+  // split sizes keep the rows kernel.
   if (block_keys == 0 && p.D == 128 && (uint64_t)B <= kernels::kStreamMaxBatch &&
-      32 * (uint64_t)std::max(k->stride[1], v->stride[1]) * 2 < (1ull << 32) &&
-      q->stride[2] == 1 && k->stride[3] == 1 && v->stride[3] == 1) {
+      32 * (uint64_t)std::max(k->stride[1], v->stride[1]) * 2 < (1ull << 32)) {
     const uint32_t chunk = kernels::stream_chunk(p.G);
     const uint64_t units = (uint64_t)B * p.Hkv * (p.G / chunk);
-    const uint32_t cus = std::max<uint32_t>(batch->ctx->compute_units, 1);
-    const uint32_t workgroups = 2 * cus;
-    if (units <= batch->ctx->split_counter_count && (uint64_t)p.Hkv * (p.G / chunk) <= 0xffffu) {
-      kernels::RowsParams rp{};
-      rp.q = static_cast<const uint16_t *>(q->data);
-      rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
-      rp.k = static_cast<const uint16_t *>(k->data);
-      rp.k_seq = k->stride[0], rp.k_pos = k->stride[1], rp.k_head = k->stride[2];
-      rp.v = static_cast<const uint16_t *>(v->data);
-      rp.v_seq = v->stride[0], rp.v_pos = v->stride[1], rp.v_head = v->stride[2];
-      rp.out = static_cast<uint16_t *>(out->data);
-      rp.o_seq = out->stride[0], rp.o_tok = 0, rp.o_head = out->stride[1];
-      rp.lengths = static_cast<const uint32_t *>(lengths->data);
-      rp.batch = (uint32_t)B, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+    const uint32_t workgroups = 2 * std::max<uint32_t>(batch->ctx->compute_units, 1);
+    if (units <= batch->ctx->split_counter_count) {
       rp.group = p.G, rp.head_chunks = p.G / chunk;
-      rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
-      rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
       const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
       void *scratch = nullptr;
       if ((st = scratch_alloc(batch, bytes, &scratch)) != MI_OK) return st;
@@ -574,19 +573,6 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   if (block_keys == 0) block_keys = std::min<uint32_t>(768, std::max<uint32_t>(64, p.L));
   if ((st = plan_rows(batch->ctx, &p, (uint64_t)B, p.L, block_keys, 256, true)) != MI_OK)
     return st;
-  kernels::RowsParams rp{};
-  rp.q = static_cast<const uint16_t *>(q->data);
-  rp.q_seq = q->stride[0], rp.q_tok = 0, rp.q_head = q->stride[1];
-  rp.k = static_cast<const uint16_t *>(k->data);
-  rp.k_seq = k->stride[0], rp.k_pos = k->stride[1], rp.k_head = k->stride[2];
-  rp.v = static_cast<const uint16_t *>(v->data);
-  rp.v_seq = v->stride[0], rp.v_pos = v->stride[1], rp.v_head = v->stride[2];
-  rp.out = static_cast<uint16_t *>(out->data);
-  rp.o_seq = out->stride[0], rp.o_tok = 0, rp.o_head = out->stride[1];
-  rp.lengths = static_cast<const uint32_t *>(lengths->data);
-  rp.batch = (uint32_t)B, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
-  rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
-  rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
   p.kernel = "attn_rows_batched";
   return run_rows(batch, p, rp);
 }
