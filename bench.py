@@ -372,6 +372,59 @@ O_PROJ = (
 )
 
 
+# The other neighbours of the attention (qwen3.rs:704-728 / 751-752): the
+# standalone RMSNorm over the hidden size and the unfused RoPE over
+# [tokens, heads, head_dim], at one decode token and at c5's prefill chunk.
+# (label, op, shape, rotate); each is HBM-bound: read + write of the tensor
+# (+ the norm weight).
+NEIGHBOURS = (
+    ("decode rms_norm, Qwen3-32B hidden: [1, 5120]", "rms_norm", (1, 5120), 64),
+    ("prefill rms_norm, c5 (Qwen3-32B): [4096, 5120]", "rms_norm", (4096, 5120), 8),
+    ("decode rope, Qwen3-32B q: [1, 64, 128]", "rope", (1, 64, 128), 64),
+    ("prefill rope, c5 q (Qwen3-32B): [4096, 64, 128]", "rope", (4096, 64, 128), 8),
+)
+
+
+def bench_neighbours(ctx, hip, eager) -> list[dict]:
+    rng = np.random.default_rng(1)
+    results = []
+    for label, op, shape, rotate in NEIGHBOURS:
+        log(f"neighbour: {label}")
+        host = rng.standard_normal(shape).astype(np.float16).view(np.uint16)
+        xs = [ctx.tensor(host) for _ in range(rotate)]
+        out = ctx.empty(shape)
+        weight = ctx.tensor((1 + 0.1 * rng.standard_normal(shape[-1])).astype(np.float16)
+                            .view(np.uint16))
+
+        def enqueue(batch, i):
+            x = xs[i % rotate]
+            if op == "rms_norm":
+                return batch.rms_norm(x, weight, 1e-6, out=out)
+            return batch.rope(x, 3, 1_000_000.0, out=out)
+
+        b = ctx.begin_batch()
+        enqueue(b, 0)
+        b.finish()
+        calls, seconds = timed(ctx, hip, enqueue, max(rotate, 64), eager, 2)
+        name, kernel_s, _ = kernel_profile(ctx, enqueue, max(rotate, 8))
+        nbytes = 2 * 2 * int(np.prod(shape)) + (2 * shape[-1] if op == "rms_norm" else 0)
+        achieved = nbytes / kernel_s / 1e9
+        entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
+                 "kernel_us": round(kernel_s * 1e6, 3),
+                 "value": round(nbytes / seconds / 1e9, 2), "unit": "GB/s",
+                 "roofline": {"bound": "hbm", "achieved": round(achieved, 2),
+                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                              "algorithmic_bytes": nbytes}}
+        log(f"  {entry['value']} GB/s, {name} {entry['kernel_us']} us")
+        results.append(entry)
+        for x in xs:
+            x.free()
+        out.free()
+        weight.free()
+    return results
+
+
 def bench_o_proj(ctx, hip, eager) -> list[dict]:
     rng = np.random.default_rng(0)
     results = []
@@ -538,6 +591,7 @@ def main() -> int:
         result["prefill"] = prefill
     if "o_proj" in chosen:
         result["o_proj"] = bench_o_proj(ctx, hip, args.eager)
+        result["neighbours"] = bench_neighbours(ctx, hip, args.eager)
     if args.copy_calibration:
         result["copy_calibration"] = copy_calibration(ctx, hip)
     if not args.no_cpu and dc is not None:

@@ -36,7 +36,11 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
 
 // rms_norm_f16 (transformer.metal:1318-1340): one wave per row, four rows per
 // workgroup. Pass 1 sums squares (16-byte loads when rows allow), pass 2
-// re-reads the row (an L1/L2 hit) and writes f16(x * scale * w).
+// writes f16(x * scale * w). Rows of up to kRmsCached 16-byte pieces per
+// lane (8192 halves) are loaded once, all pieces in flight together, and kept
+// in registers for pass 2; wider rows re-read (an L1/L2 hit).
+constexpr int kRmsCached = 16;
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -45,6 +49,38 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
   const uint16_t *x = p.x + row_offset(p.x_rows, row);
   uint16_t *out = p.out + row_offset(p.o_rows, row);
   float sum = 0.0f;
+  if constexpr (VEC) {
+    if (p.width <= 512u * kRmsCached) {
+      uint4 v[kRmsCached];
+#pragma unroll
+      for (int j = 0; j < kRmsCached; ++j) {
+        const uint32_t i = lane * 8 + 512 * j;
+        v[j] = i < p.width ? load16(x + i) : make_uint4(0, 0, 0, 0);
+      }
+      // Same order as the streaming loop below (zero pieces add exactly 0).
+#pragma unroll
+      for (int j = 0; j < kRmsCached; ++j) sum = dot8(v[j], v[j], sum);
+      sum = group_sum<64>(sum);
+      const float scale = 1.0f / sqrtf(sum / (float)p.width + p.epsilon);
+#pragma unroll
+      for (int j = 0; j < kRmsCached; ++j) {
+        const uint32_t i = lane * 8 + 512 * j;
+        if (i < p.width) {
+          const uint4 w = load16(p.weight + i);
+          const uint32_t vin[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, win[4] = {w.x, w.y, w.z, w.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint16_t lo = f32_to_f16(lo_f16(vin[e]) * scale * lo_f16(win[e]));
+            const uint16_t hi = f32_to_f16(hi_f16(vin[e]) * scale * hi_f16(win[e]));
+            o[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+          }
+          *reinterpret_cast<uint4 *>(out + i) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+      return;
+    }
+  }
   if constexpr (VEC) {
     for (uint32_t i = lane * 8; i < p.width; i += 512) {
       const uint4 v = load16(x + i);
@@ -77,27 +113,64 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
   }
 }
 
-// rope_f16 (transformer.metal:1514-1531): one thread per (token, head, pair),
-// pairs (i, i + D/2) rotated by (token + offset) * theta^(-2i/D). The same
-// f32 operations, uncontracted, as the fused Q/K kernel's RoPE step.
+// rope_f16 (transformer.metal:1514-1531): pairs (i, i + D/2) rotated by
+// (token + offset) * theta^(-2i/D). The same f32 operations, uncontracted,
+// as the fused Q/K kernel's RoPE step.
+constexpr uint32_t kRopeHeads = 8;  // heads per thread
+
+// One thread per (token, chunk of kRopeHeads heads, PAIRS consecutive
+// pairs): the angles' cosines and sines depend on (token, pair) only, so
+// they are computed once for the chunk's heads. A wave covers consecutive
+// pairs of one row, so each head's two halves load and store as contiguous
+// runs (PAIRS = 2: 4-byte accesses, 256 bytes per wave).
+template <int PAIRS>
 __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
 #pragma clang fp contract(off)
   const uint32_t half = p.head_dim / 2;
-  const uint64_t total = (uint64_t)p.tokens * p.heads * half;
+  const uint32_t groups = half / PAIRS;
+  const uint32_t chunks = (p.heads + kRopeHeads - 1) / kRopeHeads;
+  const uint64_t total = (uint64_t)p.tokens * chunks * groups;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t pair = (uint32_t)(i % half);
-    const uint64_t r = i / half;
-    const uint32_t head = (uint32_t)(r % p.heads);
-    const uint32_t token = (uint32_t)(r / p.heads);
-    const uint16_t *x = p.x + (int64_t)token * p.x_tok + (int64_t)head * p.x_head;
-    uint16_t *out = p.out + (int64_t)token * p.o_tok + (int64_t)head * p.o_head;
-    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
-    const float angle = (float)(token + p.offset) * frequency;
-    const float c = cosf(angle), s = sinf(angle);
-    const float a = f16_to_f32(x[pair]), b = f16_to_f32(x[pair + half]);
-    out[pair] = f32_to_f16(a * c - b * s);
-    out[pair + half] = f32_to_f16(a * s + b * c);
+    const uint32_t pair = (uint32_t)(i % groups) * PAIRS;
+    const uint64_t r = i / groups;
+    const uint32_t chunk = (uint32_t)(r % chunks);
+    const uint32_t token = (uint32_t)(r / chunks);
+    float c[PAIRS], s[PAIRS];
+#pragma unroll
+    for (int e = 0; e < PAIRS; ++e) {
+      const float frequency = powf(p.theta, -(float)((pair + e) * 2) / (float)p.head_dim);
+      const float angle = (float)(token + p.offset) * frequency;
+      c[e] = cosf(angle);
+      s[e] = sinf(angle);
+    }
+    const uint16_t *x = p.x + (int64_t)token * p.x_tok + pair;
+    uint16_t *out = p.out + (int64_t)token * p.o_tok + pair;
+#pragma unroll
+    for (uint32_t j = 0; j < kRopeHeads; ++j) {
+      const uint32_t head = chunk * kRopeHeads + j;
+      if (head < p.heads) {
+        const uint16_t *xa = x + (int64_t)head * p.x_head;
+        uint16_t *oa = out + (int64_t)head * p.o_head;
+        if constexpr (PAIRS == 2) {
+          const uint32_t wa = *reinterpret_cast<const uint32_t *>(xa);
+          const uint32_t wb = *reinterpret_cast<const uint32_t *>(xa + half);
+          float a[2] = {lo_f16(wa), hi_f16(wa)}, bb[2] = {lo_f16(wb), hi_f16(wb)};
+          uint32_t lo = 0, hi = 0;
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            lo |= (uint32_t)f32_to_f16(a[e] * c[e] - bb[e] * s[e]) << (16 * e);
+            hi |= (uint32_t)f32_to_f16(a[e] * s[e] + bb[e] * c[e]) << (16 * e);
+          }
+          *reinterpret_cast<uint32_t *>(oa) = lo;
+          *reinterpret_cast<uint32_t *>(oa + half) = hi;
+        } else {
+          const float a = f16_to_f32(xa[0]), bb = f16_to_f32(xa[half]);
+          oa[0] = f32_to_f16(a * c[0] - bb * s[0]);
+          oa[half] = f32_to_f16(a * s[0] + bb * c[0]);
+        }
+      }
+    }
   }
 }
 
@@ -182,11 +255,18 @@ hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l) {
 }
 
 hipError_t launch_rope(const RopeParams &p, const Launch &l) {
-  const uint64_t items = (uint64_t)p.tokens * p.heads * (p.head_dim / 2);
+  // 4-byte accesses when every row start and both halves are 4-byte aligned.
+  const bool two = p.head_dim % 4 == 0 && p.x_tok % 2 == 0 && p.x_head % 2 == 0 &&
+                   p.o_tok % 2 == 0 && p.o_head % 2 == 0 &&
+                   reinterpret_cast<uintptr_t>(p.x) % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(p.out) % 4 == 0;
+  const uint64_t items = (uint64_t)p.tokens * ((p.heads + kRopeHeads - 1) / kRopeHeads) *
+                         (p.head_dim / 2 / (two ? 2 : 1));
   if (items == 0) return no_dispatch(l);
   const uint64_t blocks64 = (items + 255) / 256;
   const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
-  return dispatch(rope_kernel, dim3(blocks), dim3(256), 0, l, p);
+  if (two) return dispatch(rope_kernel<2>, dim3(blocks), dim3(256), 0, l, p);
+  return dispatch(rope_kernel<1>, dim3(blocks), dim3(256), 0, l, p);
 }
 
 hipError_t launch_matvec(const MatvecParams &p, const Launch &l) {
