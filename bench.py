@@ -422,7 +422,51 @@ def bench_neighbours(ctx, hip, eager) -> list[dict]:
             x.free()
         out.free()
         weight.free()
+    results.append(bench_qk_norm_rope_prefill(ctx, hip, eager, rng))
     return results
+
+
+def bench_qk_norm_rope_prefill(ctx, hip, eager, rng) -> dict:
+    """The fused per-head Q/K RMSNorm + RoPE with K written into the cache
+    (qk_norm_rope_cache, qwen3.rs:704-715) over c5's 4096-token chunk."""
+    T, hq, hkv, d = 4096, 64, 8, 128
+    label = f"prefill qk_norm_rope_cache, c5 (Qwen3-32B): Q [{T}, {hq}, {d}], K [{T}, {hkv}, {d}]"
+    log(f"neighbour: {label}")
+    rotate = 4
+    qs = [ctx.tensor(rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16))
+          for _ in range(rotate)]
+    ks = [ctx.tensor(rng.standard_normal((T, hkv, d)).astype(np.float16).view(np.uint16))
+          for _ in range(rotate)]
+    w = ctx.tensor((1 + 0.1 * rng.standard_normal(d)).astype(np.float16).view(np.uint16))
+    cache = ctx.kv_cache(1, hkv, d, T)
+    key, _ = cache.layer(0)
+    q_out = ctx.empty((T, hq, d))
+    cfg = mi_attn.QkNormRopeCacheConfig(0, 1_000_000.0, 1e-6)
+
+    def enqueue(batch, i):
+        return batch.qk_norm_rope_cache(qs[i % rotate], ks[i % rotate], w, w, key, cfg,
+                                        out=q_out)
+
+    b = ctx.begin_batch()
+    enqueue(b, 0)
+    b.finish()
+    calls, seconds = timed(ctx, hip, enqueue, 16, eager, 2)
+    name, kernel_s, _ = kernel_profile(ctx, enqueue, 8)
+    nbytes = 2 * 2 * T * (hq + hkv) * d + 2 * 2 * d
+    achieved = nbytes / kernel_s / 1e9
+    entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
+             "kernel_us": round(kernel_s * 1e6, 3), "value": round(nbytes / seconds / 1e9, 2),
+             "unit": "GB/s",
+             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                          "traffic": None, "algorithmic_bytes": nbytes}}
+    log(f"  {entry['value']} GB/s, {name} {entry['kernel_us']} us")
+    for t in qs + ks:
+        t.free()
+    w.free()
+    q_out.free()
+    cache.close()
+    return entry
 
 
 def bench_o_proj(ctx, hip, eager) -> list[dict]:

@@ -146,6 +146,146 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(QkNormRopeParams p) {
   }
 }
 
+// The same operations for head_dim HD in {128, 256}, with HPW head rows of
+// one token per wave, two rows per load: lane (r, q) (r = lane / 32) holds
+// elements EPL q .. EPL q + EPL - 1 of row r of each pair of rows, as one
+// 8- or 16-byte access. Lanes q < 16 hold first halves (pairs EPL q + e),
+// lanes q >= 16 the matching second halves, so a pair's partner is lane
+// q ^ 16 (v_permlane16_swap). The angles' cosines and sines depend on token
+// and pair only and are computed once per wave (one per lane, then
+// shuffled); all rows are loaded before any is written. Per element the f32 steps are the generic kernel's; the
+// row sum adds the squares in another order.
+template <int HD, int HPW>
+__global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams p) {
+#pragma clang fp contract(off)
+  constexpr int EPL = HD / 32, HALF = HD / 2, WORDS = EPL / 2;
+  static_assert(HPW % 2 == 0, "two rows per load");
+  const uint32_t lane = threadIdx.x;
+  const uint32_t q_chunks = (p.q_heads + HPW - 1) / HPW;
+  const uint32_t k_chunks = (p.kv_heads + HPW - 1) / HPW;
+  const uint32_t qk_groups = p.tokens * (q_chunks + k_chunks);
+  const uint32_t group = blockIdx.x;
+  if (group >= qk_groups) {
+    const uint32_t row = group - qk_groups;
+    const uint32_t token = row / p.kv_heads, head = row % p.kv_heads;
+    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head;
+    uint16_t *dst = p.v_cache + (int64_t)(p.offset + token) * p.vc_pos + (int64_t)head * p.vc_head;
+    for (uint32_t i = lane; i < HD; i += 64) dst[i] = src[i];
+    return;
+  }
+  const uint32_t q_groups = p.tokens * q_chunks;
+  const bool is_query = group < q_groups;
+  const uint32_t chunk_row = is_query ? group : group - q_groups;
+  const uint32_t chunks = is_query ? q_chunks : k_chunks;
+  const uint32_t heads = is_query ? p.q_heads : p.kv_heads;
+  const uint32_t token = chunk_row / chunks;
+  const uint32_t h0 = (chunk_row % chunks) * HPW;
+  const uint16_t *weight = is_query ? p.q_weight : p.k_weight;
+  const uint32_t r = lane >> 5, q = lane & 31;
+  const bool first = q < 16;
+  const uint32_t e0 = EPL * q;  // this lane's first element of a row
+
+  // Each angle once per wave (lane l: pairs l + 64 a), then gathered by the
+  // lanes whose elements use it.
+  constexpr int APL = HALF / 64;
+  float ca[APL], sa[APL];
+#pragma unroll
+  for (int a = 0; a < APL; ++a) {
+    const uint32_t pair = lane + 64 * a;
+    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)HD);
+    const float angle = (float)(token + p.offset) * frequency;
+    ca[a] = cosf(angle);
+    sa[a] = sinf(angle);
+  }
+  float c[EPL], s[EPL], w[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const uint32_t pair = EPL * (q & 15) + e;
+    const int src = (int)(pair & 63);
+    if constexpr (APL == 1) {
+      c[e] = __shfl(ca[0], src, 64);
+      s[e] = __shfl(sa[0], src, 64);
+    } else {
+      const float c0 = __shfl(ca[0], src, 64), c1 = __shfl(ca[1], src, 64);
+      const float s0 = __shfl(sa[0], src, 64), s1 = __shfl(sa[1], src, 64);
+      c[e] = pair >= 64 ? c1 : c0;
+      s[e] = pair >= 64 ? s1 : s0;
+    }
+    w[e] = f16_to_f32(weight[e0 + e]);
+  }
+  typedef uint32_t words_t[WORDS];
+  auto row_ptr = [&](uint32_t head) -> const uint16_t * {
+    return is_query ? p.q + (int64_t)token * p.q_tok + (int64_t)head * p.q_head
+                    : p.k + (int64_t)token * p.k_tok + (int64_t)head * p.k_head;
+  };
+  uint32_t v[HPW / 2][WORDS];
+#pragma unroll
+  for (int i = 0; i < HPW / 2; ++i) {
+    const uint32_t head = h0 + 2 * i + r;
+    if (head < heads) {
+      const uint16_t *src = row_ptr(head) + e0;
+      if constexpr (WORDS == 4) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(src);
+        v[i][0] = x.x, v[i][1] = x.y, v[i][2] = x.z, v[i][3] = x.w;
+      } else {
+        const uint2 x = *reinterpret_cast<const uint2 *>(src);
+        v[i][0] = x.x, v[i][1] = x.y;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < WORDS; ++k) v[i][k] = 0;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < HPW / 2; ++i) {
+    const uint32_t head = h0 + 2 * i + r;
+    float x[EPL];
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      x[e] = (e & 1) ? hi_f16(v[i][e >> 1]) : lo_f16(v[i][e >> 1]);
+      sum += x[e] * x[e];
+    }
+    // Row sum over the 32 lanes of this row.
+    for (int mask = 16; mask > 0; mask >>= 1) sum += __shfl_xor(sum, mask, 64);
+    const float scale = 1.0f / sqrtf(sum / (float)HD + p.epsilon);
+    float n[EPL], m[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) n[e] = x[e] * scale * w[e];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(n[e]), __float_as_uint(n[e]),
+                                                        false, false);
+      // The value from the other 16-lane row is whichever output differs
+      // from this lane's own input slot.
+      m[e] = __uint_as_float((lane & 16) ? sw[0] : sw[1]);
+    }
+    if (head < heads) {
+      uint16_t *dst =
+          (is_query ? p.q_out + (int64_t)token * p.qo_tok + (int64_t)head * p.qo_head
+                    : p.cache + (int64_t)(p.offset + token) * p.c_pos + (int64_t)head * p.c_head) +
+          e0;
+      uint32_t o[WORDS];
+#pragma unroll
+      for (int k = 0; k < WORDS; ++k) {
+        uint16_t hv[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int e = 2 * k + t;
+          // First halves: x c - y s with y the partner's; second halves:
+          // x s + y c with x the partner's.
+          hv[t] = first ? f32_to_f16(n[e] * c[e] - m[e] * s[e]) : f32_to_f16(m[e] * s[e] + n[e] * c[e]);
+        }
+        o[k] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
+      }
+      if constexpr (WORDS == 4)
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+      else
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(o[0], o[1]);
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_naive(const NaiveParams &p, uint32_t row_begin,
@@ -171,7 +311,35 @@ hipError_t launch_copy_kv(const CopyKvParams &p, const Launch &l) {
   return dispatch(copy_kv_kernel<1>, dim3(blocks), dim3(256), 0, l, p);
 }
 
+namespace {
+template <int HD, int HPW>
+hipError_t launch_qk_rows(const QkNormRopeParams &p, const Launch &l) {
+  const uint32_t chunks = (p.q_heads + HPW - 1) / HPW + (p.kv_heads + HPW - 1) / HPW;
+  const uint32_t groups = p.tokens * chunks + (p.v != nullptr ? p.tokens * p.kv_heads : 0u);
+  if (groups == 0) return no_dispatch(l);
+  return dispatch(qk_norm_rope_rows_kernel<HD, HPW>, dim3(groups), dim3(64), 0, l, p);
+}
+}  // namespace
+
 hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
+  // Many tokens (prefill): 16 head rows per wave share the angles (8: 48.8,
+  // 16: 46.2, 32: 47.3 us on c5's chunk). Few tokens
+  // (decode): two rows per wave, for the most waves in flight. Needs 8- or
+  // 16-byte aligned rows.
+  const bool many = p.tokens >= 16;
+  const uint32_t vec = p.head_dim / 32;
+  const bool aligned = (p.head_dim == 128 || p.head_dim == 256) && p.q_tok % vec == 0 &&
+                       p.q_head % vec == 0 && p.k_tok % vec == 0 && p.k_head % vec == 0 &&
+                       p.qo_tok % vec == 0 && p.qo_head % vec == 0 && p.c_pos % vec == 0 &&
+                       p.c_head % vec == 0 &&
+                       reinterpret_cast<uintptr_t>(p.q) % (2 * vec) == 0 &&
+                       reinterpret_cast<uintptr_t>(p.k) % (2 * vec) == 0 &&
+                       reinterpret_cast<uintptr_t>(p.q_out) % (2 * vec) == 0 &&
+                       reinterpret_cast<uintptr_t>(p.cache) % (2 * vec) == 0;
+  if (aligned && p.head_dim == 128)
+    return many ? launch_qk_rows<128, 16>(p, l) : launch_qk_rows<128, 2>(p, l);
+  if (aligned && p.head_dim == 256)
+    return many ? launch_qk_rows<256, 16>(p, l) : launch_qk_rows<256, 2>(p, l);
   const uint32_t groups =
       p.tokens * (p.q_heads + p.kv_heads) + (p.v != nullptr ? p.tokens * p.kv_heads : 0u);
   if (groups == 0) return no_dispatch(l);

@@ -117,6 +117,26 @@ def test_qk_norm_rope_cache_seeded(ctx, offset):
         assert diff.max() <= max(2e-3, 2e-3 * mag), (offset, diff.max())
 
 
+@pytest.mark.parametrize("T,hq,hkv,d,offset", [
+    (37, 20, 3, 128, 11),   # 16 rows per wave, ragged head chunks, odd KV heads
+    (19, 8, 2, 256, 500),   # head_dim 256, 16 rows per wave
+    (5, 6, 1, 256, 0),      # few tokens: two rows per wave
+    (3, 5, 3, 128, 2),      # odd counts in both row pairs
+])
+def test_qk_norm_rope_cache_row_layouts(ctx, T, hq, hkv, d, offset):
+    theta, eps = 1_000_000.0, 1e-6
+    q, k = rand(60 + T, (T, hq, d)), rand(61 + T, (T, hkv, d))
+    qw = (1 + 0.1 * np.random.default_rng(62).standard_normal(d)).astype(np.float16).view(np.uint16)
+    kw = (1 + 0.1 * np.random.default_rng(63).standard_normal(d)).astype(np.float16).view(np.uint16)
+    got_q, got_cache = _qk_case(ctx, q, k, qw, kw, offset, theta, eps, offset + T + 2)
+    want_q, want_k = oracle.qk_norm_rope(q, k, qw, kw, offset=offset, theta=theta, epsilon=eps)
+    for got, want in ((got_q, want_q), (got_cache[offset:offset + T], want_k)):
+        diff = np.abs(f16(got).astype(np.float64) - f16(want))
+        mag = np.abs(f16(want)).max()
+        assert diff.max() <= max(2e-3, 2e-3 * mag), (T, hq, hkv, d, diff.max())
+    assert (got_cache[:offset] == 0).all() and (got_cache[offset + T:] == 0).all()
+
+
 def test_decode_loop_in_forward_layer_order(ctx):
     """Per step: Q/K norm+RoPE with K into the cache, V appended, then
     attention over the cache prefix (qwen3.rs:704-750), all in one batch."""
