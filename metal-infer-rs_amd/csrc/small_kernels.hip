@@ -166,11 +166,18 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
   const uint32_t qk_groups = p.tokens * (q_chunks + k_chunks);
   const uint32_t group = blockIdx.x;
   if (group >= qk_groups) {
-    const uint32_t row = group - qk_groups;
+    // Value rows, two per wave (lanes 0-31 and 32-63), one 8- or 16-byte
+    // piece per lane.
+    const uint32_t row = 2 * (group - qk_groups) + (lane >> 5);
+    if (row >= p.tokens * p.kv_heads) return;
     const uint32_t token = row / p.kv_heads, head = row % p.kv_heads;
-    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head;
-    uint16_t *dst = p.v_cache + (int64_t)(p.offset + token) * p.vc_pos + (int64_t)head * p.vc_head;
-    for (uint32_t i = lane; i < HD; i += 64) dst[i] = src[i];
+    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head + EPL * (lane & 31);
+    uint16_t *dst = p.v_cache + (int64_t)(p.offset + token) * p.vc_pos + (int64_t)head * p.vc_head +
+                    EPL * (lane & 31);
+    if constexpr (WORDS == 4)
+      *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+    else
+      *reinterpret_cast<uint2 *>(dst) = *reinterpret_cast<const uint2 *>(src);
     return;
   }
   const uint32_t q_groups = p.tokens * q_chunks;
@@ -213,7 +220,6 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
     }
     w[e] = f16_to_f32(weight[e0 + e]);
   }
-  typedef uint32_t words_t[WORDS];
   auto row_ptr = [&](uint32_t head) -> const uint16_t * {
     return is_query ? p.q + (int64_t)token * p.q_tok + (int64_t)head * p.q_head
                     : p.k + (int64_t)token * p.k_tok + (int64_t)head * p.k_head;
@@ -315,7 +321,7 @@ namespace {
 template <int HD, int HPW>
 hipError_t launch_qk_rows(const QkNormRopeParams &p, const Launch &l) {
   const uint32_t chunks = (p.q_heads + HPW - 1) / HPW + (p.kv_heads + HPW - 1) / HPW;
-  const uint32_t groups = p.tokens * chunks + (p.v != nullptr ? p.tokens * p.kv_heads : 0u);
+  const uint32_t groups = p.tokens * chunks + (p.v != nullptr ? (p.tokens * p.kv_heads + 1) / 2 : 0u);
   if (groups == 0) return no_dispatch(l);
   return dispatch(qk_norm_rope_rows_kernel<HD, HPW>, dim3(groups), dim3(64), 0, l, p);
 }
@@ -325,7 +331,7 @@ hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
   // Many tokens (prefill): 16 head rows per wave share the angles (8: 48.8,
   // 16: 46.2, 32: 47.3 us on c5's chunk). Few tokens
   // (decode): two rows per wave, for the most waves in flight. Needs 8- or
-  // 16-byte aligned rows.
+  // 16-byte aligned rows (value rows included when the value is appended).
   const bool many = p.tokens >= 16;
   const uint32_t vec = p.head_dim / 32;
   const bool aligned = (p.head_dim == 128 || p.head_dim == 256) && p.q_tok % vec == 0 &&
@@ -335,7 +341,11 @@ hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
                        reinterpret_cast<uintptr_t>(p.q) % (2 * vec) == 0 &&
                        reinterpret_cast<uintptr_t>(p.k) % (2 * vec) == 0 &&
                        reinterpret_cast<uintptr_t>(p.q_out) % (2 * vec) == 0 &&
-                       reinterpret_cast<uintptr_t>(p.cache) % (2 * vec) == 0;
+                       reinterpret_cast<uintptr_t>(p.cache) % (2 * vec) == 0 &&
+                       (p.v == nullptr ||
+                        (p.v_tok % vec == 0 && p.v_head % vec == 0 && p.vc_pos % vec == 0 &&
+                         p.vc_head % vec == 0 && reinterpret_cast<uintptr_t>(p.v) % (2 * vec) == 0 &&
+                         reinterpret_cast<uintptr_t>(p.v_cache) % (2 * vec) == 0));
   if (aligned && p.head_dim == 128)
     return many ? launch_qk_rows<128, 16>(p, l) : launch_qk_rows<128, 2>(p, l);
   if (aligned && p.head_dim == 256)

@@ -204,11 +204,16 @@ def _fused_vs_pair(ctx, T, offset, capacity, hq=16, hkv=8, d=128):
     return results, v
 
 
-@pytest.mark.parametrize("T,offset,capacity", [(1, 2047, 2048), (5, 300, 512), (3, 0, 3)])
-def test_fused_value_append_matches_the_two_calls(ctx, T, offset, capacity):
+@pytest.mark.parametrize("T,offset,capacity,hq,hkv,d", [
+    (1, 2047, 2048, 16, 8, 128), (5, 300, 512, 16, 8, 128), (3, 0, 3, 16, 8, 128),
+    (5, 7, 16, 6, 3, 256),       # odd number of value rows
+    (37, 100, 160, 20, 3, 128),  # 16 rows per wave
+    (4, 1, 8, 4, 2, 64),         # head_dim 64: the generic kernel
+])
+def test_fused_value_append_matches_the_two_calls(ctx, T, offset, capacity, hq, hkv, d):
     """mi_qk_norm_rope_cache_value == qk_norm_rope_cache then
     copy_into_cache(value), bit for bit (qwen3.rs:704-728 order)."""
-    (pair, fused), v = _fused_vs_pair(ctx, T, offset, capacity)
+    (pair, fused), v = _fused_vs_pair(ctx, T, offset, capacity, hq, hkv, d)
     for a, b in zip(pair, fused):
         assert (a == b).all()
     assert (fused[2][offset:offset + T] == v).all()
