@@ -267,6 +267,27 @@ def bench_decode_step(ctx, hip, steps):
     del keep
     graph_us = ms.value * 1e3 / (reps * PER_GRAPH)
 
+    def graph_us_of(step):
+        """GPU time per step of PER_GRAPH captured steps, replayed."""
+        capture = ctx.begin_capture()
+        kept = [step(capture, i) for i in range(PER_GRAPH)]
+        g = capture.end_capture()
+        g.launch()
+        ctx.synchronize()
+        b = ctx.begin_batch()
+        s = ctypes.c_void_p(b.stream)
+        hip.check(hip.lib.hipEventRecord(start, s), "record")
+        for _ in range(reps):
+            g.launch()
+        hip.check(hip.lib.hipEventRecord(end, s), "record")
+        hip.check(hip.lib.hipEventSynchronize(end), "sync")
+        b.finish()
+        elapsed = ctypes.c_float()
+        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(elapsed), start, end), "elapsed")
+        g.destroy()
+        del kept
+        return elapsed.value * 1e3 / (reps * PER_GRAPH)
+
     # The same step with the V append folded into the Q/K kernel
     # (mi_qk_norm_rope_cache_value): two kernels.
     def enqueue_fused(batch, i):
@@ -275,28 +296,21 @@ def bench_decode_step(ctx, hip, steps):
         return batch.attention(q_rot, key.prefix(L), value.prefix(L), cfg, mi_attn.FLASH_DECODE,
                                out=out)
 
-    capture = ctx.begin_capture()
-    keep = [enqueue_fused(capture, i) for i in range(PER_GRAPH)]
-    graph = capture.end_capture()
-    graph.launch()
-    ctx.synchronize()
-    batch = ctx.begin_batch()
-    stream = ctypes.c_void_p(batch.stream)
-    hip.check(hip.lib.hipEventRecord(start, stream), "record")
-    for _ in range(reps):
-        graph.launch()
-    hip.check(hip.lib.hipEventRecord(end, stream), "record")
-    hip.check(hip.lib.hipEventSynchronize(end), "sync")
-    batch.finish()
-    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, end), "elapsed")
-    graph.destroy()
-    del keep
+    # The whole step in one launch (mi_decode_step_attention): the Q/K
+    # transforms run inside the attention kernel.
+    def enqueue_step(batch, i):
+        return batch.decode_step_attention(q_in, k_in, v_in, weights, weights, key, value, rope,
+                                           cfg, out=out)
+
+    fused_value_us = graph_us_of(enqueue_fused)
+    one_launch_us = graph_us_of(enqueue_step)
     cache.close()
     return {"workload": "c2 decode step: qk_norm_rope_cache + copy_into_cache + FlashDecode "
                         f"(3 kernels), same cache slot every step; {PER_GRAPH} steps per "
                         "captured graph",
             "graph_us": round(graph_us, 3), "eager_us": round(eager * 1e6, 3),
-            "graph_fused_value_us": round(ms.value * 1e3 / (reps * PER_GRAPH), 3)}
+            "graph_fused_value_us": round(fused_value_us, 3),
+            "graph_one_launch_us": round(one_launch_us, 3)}
 
 
 def bench_batched_decode(ctx, hip, steps, eager):
@@ -600,7 +614,8 @@ def main() -> int:
     if "c2" in chosen and not args.eager:
         result["decode_step"] = bench_decode_step(ctx, hip, 256)
         log(f"decode step: graph {result['decode_step']['graph_us']} us "
-            f"(fused value append {result['decode_step']['graph_fused_value_us']} us), "
+            f"(fused value append {result['decode_step']['graph_fused_value_us']} us, "
+            f"one launch {result['decode_step']['graph_one_launch_us']} us), "
             f"eager {result['decode_step']['eager_us']} us")
     if "c4" in chosen:
         bc, bat = bench_batched_decode(ctx, hip, 20, args.eager)

@@ -345,6 +345,27 @@ mi_status mi_qk_norm_rope_cache_value(mi_batch *batch, const mi_tensor *q,
                                       const mi_qk_norm_rope_cache_config *config,
                                       const mi_tensor *q_out);
 
+/* One decode token's attention step in one launch: qk_norm_rope_cache, the
+ * value's copy_into_cache and FlashDecode attention over the cache prefix
+ * [0, qk_config->offset] (key_cache / value_cache [capacity, Hkv, D]), the
+ * three calls forward_layer issues per layer and token (crates/
+ * metal-infer-models/src/qwen3.rs:704-750; ops.rs:917-994, 1249-1285). No
+ * counterpart in the reference as one call. q / k / value are [1, H, D];
+ * the rotated query is not returned; out [1, Hq, D] gets the attention.
+ * config->query_offset must equal qk_config->offset. Errors are those of the
+ * three calls. At head_dim 128 with 16-byte aligned rows (and the library's
+ * default decode split) the query and key transforms run inside the
+ * attention kernel; otherwise the three calls' kernels run in order. */
+mi_status mi_decode_step_attention(mi_batch *batch, const mi_tensor *q,
+                                   const mi_tensor *k, const mi_tensor *value,
+                                   const mi_tensor *q_weight,
+                                   const mi_tensor *k_weight,
+                                   const mi_tensor *key_cache,
+                                   const mi_tensor *value_cache,
+                                   const mi_qk_norm_rope_cache_config *qk_config,
+                                   const mi_attention_config *config,
+                                   const mi_tensor *out);
+
 /* ------------------------------------------------ attention neighbours -- */
 
 /* The steps on either side of attention in Qwen3's forward_layer

@@ -175,10 +175,51 @@ __device__ __forceinline__ void merge_splits(const RowsParams &p, uint32_t unit,
                                         nsplits, out, p.o_head, buf);
 }
 
+// qk_norm_rope_cache's per-head transform (ops.rs:917-977,
+// transformer.metal:1533-1577) of one D = 128 row held as the rows kernel
+// holds it: 16 lanes, lane `col` with elements 8 col .. 8 col + 7 (and the
+// same elements of the weight). The RoPE partner of element d < 64 is d + 64,
+// held by lane col ^ 8 (first: col < 8); cs / sn are the cosines and sines of
+// this lane's 8 pairs. Per element the f32 steps are
+// those of qk_norm_rope_kernel; the row sum adds the squares in another order.
+__device__ __forceinline__ Vec<8> norm_rope_row(const Vec<8> &raw, const Vec<8> &weight,
+                                                const float *cs, const float *sn, float eps,
+                                                bool first) {
+#pragma clang fp contract(off)
+  float x[8], n[8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[e] = elem<8>(raw, e);
+    sum += x[e] * x[e];
+  }
+  sum = lane_group_sum<16>(sum);
+  const float scale = 1.0f / sqrtf(sum / 128.0f + eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = x[e] * scale * elem<8>(weight, e);
+  Vec<8> r;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t h[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = 2 * w + t;
+      const float m = dpp_f32<kDppRowRor8>(n[e]);  // lane col ^ 8 of the 16
+      // First halves x c - y s, second halves y s + x c (y, x: partner's),
+      // both as n c + (-+ m s) without a branch.
+      const float ms = m * sn[e];
+      h[t] = f32_to_f16(n[e] * cs[e] + (first ? -ms : ms));
+    }
+    r.w[w] = h[0] | (h[1] << 16);
+  }
+  return r;
+}
+
 // FUSED: with more than one split, each split publishes its partial with
 // device-scope stores and counts its arrival in p.counters[unit]; the last
 // split to arrive merges all of them in split order (no second launch).
-template <int D, int WAVES, int GC, bool FUSED>
+// STEP: the decode step (RowsParams::step_k), D = 128 and one token only.
+template <int D, int WAVES, int GC, bool FUSED, bool STEP = false>
 __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     const RowsParams p) {
   constexpr int VEC = D >= 8 ? 8 : D;  // halves per lane per key row
@@ -239,6 +280,19 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
                          (int64_t)h0 * p.q_head + col * VEC;
 #pragma unroll
     for (int g = 0; g < GC; ++g) qv[g] = load_vec<VEC>(qb + g * p.q_head);
+  }
+  // STEP: the new key (raw, then transformed) and value rows of head kvh,
+  // loaded ahead of the cache rows so their wait leaves those in flight.
+  Vec<VEC> kr, vr, wq, wk;
+  if constexpr (STEP) {
+    static_assert(D == 128 && VEC == 8, "decode step: head_dim 128");
+    kr = load_vec<VEC>(p.step_k + (int64_t)kvh * p.step_k_head + col * VEC);
+    vr = load_vec<VEC>(p.step_v + (int64_t)kvh * p.step_v_head + col * VEC);
+    wq = load_vec<VEC>(p.step_qw + col * VEC);
+    wk = load_vec<VEC>(p.step_kw + col * VEC);
+    // Issued before the cache rows' loads, which the transforms below must
+    // not wait for (loads complete in issue order).
+    __builtin_amdgcn_sched_barrier(0);
   }
   const uint16_t *kb =
       p.k + (int64_t)b * p.k_seq + (int64_t)kvh * p.k_head + col * VEC;
@@ -321,15 +375,83 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   // flight never has to be copied into the one being consumed.
   Vec<VEC> ka[U], va[U], kb2[U], vb2[U];
   uint32_t key = k0 + row;
-  if (key < k1) load_batch(key, ka, va);
+  // (STEP: unconditional, as the clamped rows stay in bounds, so that the
+  // waits below count only loads issued on every path.)
+  if (STEP || key < k1) load_batch(key, ka, va);
+  if constexpr (STEP) {
+    // While the cache rows are in flight: one RoPE angle per lane (pair =
+    // lane, position query_offset, as qk_norm_rope_kernel computes it),
+    // gathered by the lanes whose elements use it; then the query rows and
+    // the key row are transformed. The key's last split writes the key and
+    // value rows into the caches; it reads them from registers below.
+    // (Sharing the angles through LDS, 16 per wave, measured no faster.)
+    float ca, sa;
+    {
+#pragma clang fp contract(off)
+      const float frequency = powf(p.step_theta, -(float)(lane * 2) / (float)D);
+      const float angle = (float)p.query_offset * frequency;
+      ca = cosf(angle);
+      sa = sinf(angle);
+    }
+    float cs[8], sn[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      cs[e] = __shfl(ca, 8 * (col & 7) + e, 64);
+      sn[e] = __shfl(sa, 8 * (col & 7) + e, 64);
+    }
+    // The GC query rows and the key row, one per 16-lane group (four per
+    // pass), then gathered by every group.
+    constexpr int PASSES = (GC + 1 + 3) / 4;
+    Vec<VEC> t[PASSES];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int i = 4 * ps + rloc;  // this group's row: query head i < GC, else the key
+      Vec<VEC> raw = kr, w = wk;
+#pragma unroll
+      for (int g = 0; g < GC; ++g)
+#pragma unroll
+        for (int k = 0; k < VEC / 2; ++k) {
+          raw.w[k] = i == g ? qv[g].w[k] : raw.w[k];
+          w.w[k] = i == g ? wq.w[k] : w.w[k];
+        }
+      t[ps] = norm_rope_row(raw, w, cs, sn, p.step_eps, col < 8);
+    }
+#pragma unroll
+    for (int k = 0; k < VEC / 2; ++k) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g) qv[g].w[k] = __shfl(t[g / 4].w[k], (g % 4) * LPR + col, 64);
+      kr.w[k] = __shfl(t[GC / 4].w[k], (GC % 4) * LPR + col, 64);
+    }
+    if (split == nsplits - 1 && hc == 0 && wave == 0 && rloc == 0) {
+      const int64_t pos = p.query_offset;
+      *reinterpret_cast<uint4 *>(p.step_kc + (int64_t)kvh * p.k_head + pos * p.k_pos + col * VEC) =
+          make_uint4(kr.w[0], kr.w[1], kr.w[2], kr.w[3]);
+      *reinterpret_cast<uint4 *>(p.step_vc + (int64_t)kvh * p.v_head + pos * p.v_pos + col * VEC) =
+          make_uint4(vr.w[0], vr.w[1], vr.w[2], vr.w[3]);
+    }
+  }
+  // STEP: the cache row at query_offset is read before (or while) it is
+  // written, so its lanes take the new rows from registers instead.
+  auto patch = [&](Vec<VEC> *kd, Vec<VEC> *vd, uint32_t first) __attribute__((always_inline)) {
+    if constexpr (STEP) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (first + (uint32_t)(u * R) == p.query_offset) {
+          kd[u] = kr;
+          vd[u] = vr;
+        }
+    }
+  };
   while (key < k1) {
     uint32_t next = key + R * U;
     if (next < k1) load_batch(next, kb2, vb2);
+    patch(ka, va, key);
     consume_any(ka, va, key);
     key = next;
     if (key >= k1) break;
     next = key + R * U;
     if (next < k1) load_batch(next, ka, va);
+    patch(kb2, vb2, key);
     consume_any(kb2, vb2, key);
     key = next;
   }
@@ -792,6 +914,14 @@ hipError_t launch_rows_dwg(const RowsParams &p, RowsPhase phase, const Launch &l
   if (phase == RowsPhase::Split) {
     const dim3 grid(p.max_splits, p.kv_heads * p.head_chunks,
                     p.batch * p.tokens);
+    if constexpr (D == 128 && WAVES == 8) {
+      if (p.step_k != nullptr) {
+        if (p.counters != nullptr)
+          return dispatch(attn_rows_kernel<D, WAVES, GC, true, true>, grid, dim3(WAVES * 64), 0, l, p);
+        return dispatch(attn_rows_kernel<D, WAVES, GC, false, true>, grid, dim3(WAVES * 64), 0, l, p);
+      }
+    }
+    if (p.step_k != nullptr) return hipErrorInvalidValue;
     if (p.counters != nullptr)
       return dispatch(attn_rows_kernel<D, WAVES, GC, true>, grid, dim3(WAVES * 64), 0, l, p);
     return dispatch(attn_rows_kernel<D, WAVES, GC, false>, grid, dim3(WAVES * 64), 0, l, p);

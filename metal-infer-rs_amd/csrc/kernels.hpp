@@ -65,6 +65,16 @@ struct RowsParams {
   uint32_t block_keys;      // keys per split
   uint32_t max_splits;
   float scale_log2;         // rsqrt(D) * log2(e)
+  // Decode step (step_k != null; one token, D = 128, 8 waves): q holds the
+  // raw query rows and step_k / step_v the new token's key and value rows
+  // [Hkv, D]. The kernel applies qk_norm_rope_cache's per-head RMSNorm +
+  // RoPE (position query_offset) to the query and key rows, writes the key
+  // and value rows into step_kc / step_vc (the caches k / v point into) at
+  // query_offset, and attends over keys 0 .. query_offset.
+  const uint16_t *step_k, *step_v, *step_qw, *step_kw;
+  int64_t step_k_head, step_v_head;
+  uint16_t *step_kc, *step_vc;
+  float step_theta, step_eps;
 };
 
 // Exact two-pass attention (AttentionKind::Reference).

@@ -733,4 +733,74 @@ mi_status mi_qk_norm_rope_cache_value(mi_batch *batch, const mi_tensor *q, const
                 [&](const kernels::Launch &s) { return kernels::launch_qk_norm_rope(qp, s); });
 }
 
+mi_status mi_decode_step_attention(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                                   const mi_tensor *value, const mi_tensor *q_weight,
+                                   const mi_tensor *k_weight, const mi_tensor *key_cache,
+                                   const mi_tensor *value_cache,
+                                   const mi_qk_norm_rope_cache_config *qk_config,
+                                   const mi_attention_config *config, const mi_tensor *out) {
+  if (value == nullptr || value_cache == nullptr || config == nullptr || out == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
+  // Validation of the three calls this replaces. The rotated query is not
+  // returned, so the query itself stands in for q_out's shape check.
+  kernels::QkNormRopeParams qp;
+  mi_status st = prepare_qk_norm_rope(batch, q, k, q_weight, k_weight, key_cache, qk_config, q, &qp);
+  if (st != MI_OK) return st;
+  if ((st = check_kv_append(value, value_cache, qk_config->offset)) != MI_OK) return st;
+  if (value->shape[0] != q->shape[0] || value->shape[1] != k->shape[1] ||
+      value->shape[2] != k->shape[2])
+    return fail(MI_ERR_SHAPE, "value rows must have the key's shape");
+  if (q->shape[0] != 1) return fail(MI_ERR_SHAPE, "decode attention requires exactly one query token");
+  if (config->query_offset != qk_config->offset)
+    return fail(MI_ERR_SHAPE, "decode step: the attention's query_offset must be the transform's offset");
+  // FlashDecode over the cache prefix that ends with the new token, planned
+  // with the library's default split (as for one decode token without a
+  // tuned table), whatever mi_tune_flash_decode recorded.
+  mi_tensor key = *key_cache, val = *value_cache;
+  key.shape[0] = val.shape[0] = (int64_t)qk_config->offset + 1;
+  AttnPlan p;
+  if ((st = plan_attention(batch->ctx, q, &key, &val, config, MI_ATTN_DECODE_SPLIT_KV, 0, 0, false,
+                           out, &p)) != MI_OK)
+    return st;
+  const bool fused = p.family == Family::Rows && p.D == 128 && p.waves == 8 &&
+                     vector_friendly(*k, 8) && vector_friendly(*value, 8) &&
+                     vector_friendly(*key_cache, 8) && vector_friendly(*value_cache, 8) &&
+                     reinterpret_cast<uintptr_t>(q_weight->data) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(k_weight->data) % 16 == 0;
+  if (!fused) {
+    // The same work as the three calls, in their order.
+    void *q_rot = nullptr;
+    const uint64_t q_bytes = (uint64_t)q->shape[1] * q->shape[2] * sizeof(uint16_t);
+    if ((st = scratch_alloc(batch, q_bytes, &q_rot)) != MI_OK) return st;
+    mi_tensor qr{};
+    qr.data = q_rot, qr.dtype = MI_F16, qr.rank = 3;
+    qr.shape[0] = 1, qr.shape[1] = q->shape[1], qr.shape[2] = q->shape[2];
+    qr.stride[0] = q->shape[1] * q->shape[2], qr.stride[1] = q->shape[2], qr.stride[2] = 1;
+    st = mi_qk_norm_rope_cache_value(batch, q, k, value, q_weight, k_weight, key_cache, value_cache,
+                                     qk_config, &qr);
+    if (st == MI_OK)
+      st = run_attention(batch, &qr, &key, &val, config, MI_ATTN_FLASH_DECODE, 0, 0, false, out);
+    // In-order execution makes the range reusable by later work of the batch.
+    scratch_free(batch->ctx, q_rot);
+    return st;
+  }
+  const float scale = 1.0f / std::sqrt((float)p.D);
+  kernels::RowsParams rp{};
+  rp.q = static_cast<const uint16_t *>(q->data), rp.q_tok = q->stride[0], rp.q_head = q->stride[1];
+  rp.k = static_cast<const uint16_t *>(key.data), rp.k_pos = key.stride[0], rp.k_head = key.stride[1];
+  rp.v = static_cast<const uint16_t *>(val.data), rp.v_pos = val.stride[0], rp.v_head = val.stride[1];
+  rp.out = static_cast<uint16_t *>(out->data), rp.o_tok = out->stride[0], rp.o_head = out->stride[1];
+  rp.batch = 1, rp.tokens = 1, rp.q_heads = p.Hq, rp.kv_heads = p.Hkv;
+  rp.kv_length = p.L, rp.causal = config->causal != 0, rp.query_offset = config->query_offset;
+  rp.scale_log2 = scale * 1.4426950408889634f;
+  rp.step_k = qp.k, rp.step_k_head = qp.k_head;
+  rp.step_v = static_cast<const uint16_t *>(value->data), rp.step_v_head = value->stride[1];
+  rp.step_qw = qp.q_weight, rp.step_kw = qp.k_weight;
+  rp.step_kc = static_cast<uint16_t *>(key_cache->data);
+  rp.step_vc = static_cast<uint16_t *>(value_cache->data);
+  rp.step_theta = qp.theta, rp.step_eps = qp.epsilon;
+  p.kernel = "attn_decode_step";
+  return run_rows(batch, p, rp);
+}
+
 }  // extern "C"

@@ -147,6 +147,9 @@ def _load() -> ctypes.CDLL:
                                                  _P(QkNormRopeCacheConfig), T]),
         "mi_qk_norm_rope_cache_value": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T, T, T, T,
                                                        _P(QkNormRopeCacheConfig), T]),
+        "mi_decode_step_attention": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T, T, T, T,
+                                                    _P(QkNormRopeCacheConfig),
+                                                    _P(AttentionConfig), T]),
         "mi_rms_norm": (ctypes.c_int, [ctypes.c_void_p, T, T, ctypes.c_float, T]),
         "mi_rope": (ctypes.c_int, [ctypes.c_void_p, T, ctypes.c_uint64, ctypes.c_float, T]),
         "mi_matmul": (ctypes.c_int, [ctypes.c_void_p, T, T, T]),
@@ -515,6 +518,20 @@ class Batch:
             self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(value.desc),
             ctypes.byref(q_weight.desc), ctypes.byref(k_weight.desc), ctypes.byref(key_cache.desc),
             ctypes.byref(value_cache.desc), ctypes.byref(config), ctypes.byref(out.desc)))
+        return out
+
+    def decode_step_attention(self, q, k, value, q_weight, k_weight, key_cache, value_cache,
+                              qk_config: QkNormRopeCacheConfig, config: AttentionConfig,
+                              out=None) -> Tensor:
+        """qk_norm_rope_cache, the value's copy_into_cache and FlashDecode
+        attention over the cache prefix [0, offset], as one step
+        (qwen3.rs:704-750); returns the attention output."""
+        out = self._out(q.shape, out)
+        _check(lib().mi_decode_step_attention(
+            self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(value.desc),
+            ctypes.byref(q_weight.desc), ctypes.byref(k_weight.desc), ctypes.byref(key_cache.desc),
+            ctypes.byref(value_cache.desc), ctypes.byref(qk_config), ctypes.byref(config),
+            ctypes.byref(out.desc)))
         return out
 
     def rms_norm(self, x: Tensor, weight: Tensor, epsilon: float, out=None) -> Tensor:

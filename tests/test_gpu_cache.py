@@ -278,3 +278,88 @@ def test_captured_fused_decode_step_replays_match_eager(ctx):
         assert (ctx.download(value.prefix(pos + 1))[pos] == ctx.download(v_in)[0]).all()
     graph.destroy()
     cache.close()
+
+
+# ------------------------------------------- one-launch decode attention step --
+
+@pytest.mark.parametrize("hq,hkv,d,pos", [
+    (16, 8, 128, 2047),   # c2: 16 splits merged in the launch
+    (32, 8, 128, 300),    # GQA 4
+    (64, 8, 128, 100),    # GQA 8, one split
+    (16, 8, 128, 0),      # the new token is the only key
+    (8, 8, 128, 1000),    # MHA
+    (8, 4, 64, 500),      # head_dim 64: the three calls' kernels
+])
+def test_decode_step_matches_the_three_calls(ctx, hq, hkv, d, pos):
+    """mi_decode_step_attention == qk_norm_rope_cache_value then FlashDecode
+    over the prefix [0, pos] (qwen3.rs:704-750), and both match the oracle."""
+    cap, theta, eps = pos + 3, 1_000_000.0, 1e-6
+    seed = 7 * pos + hq
+    q, k, v = rand(seed, (1, hq, d)), rand(seed + 1, (1, hkv, d)), rand(seed + 2, (1, hkv, d))
+    qw = (1 + 0.1 * np.random.default_rng(seed + 3).standard_normal(d)).astype(np.float16).view(np.uint16)
+    kw = (1 + 0.1 * np.random.default_rng(seed + 4).standard_normal(d)).astype(np.float16).view(np.uint16)
+    k_hist, v_hist = rand(seed + 5, (cap, hkv, d)), rand(seed + 6, (cap, hkv, d))
+    qt, kt, vt, qwt, kwt = (ctx.tensor(a) for a in (q, k, v, qw, kw))
+    qk_cfg = mi_attn.QkNormRopeCacheConfig(pos, theta, eps)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
+    results = []
+    for fused in (False, True):
+        cache = ctx.kv_cache(1, hkv, d, cap)
+        key, value = cache.layer(0)
+        ctx.upload(key, k_hist)
+        ctx.upload(value, v_hist)
+        ctx.take_kernel_profiles()
+        ctx.set_kernel_profiling(True)
+        try:
+            batch = ctx.begin_batch()
+            if fused:
+                out = batch.decode_step_attention(qt, kt, vt, qwt, kwt, key, value, qk_cfg, cfg)
+            else:
+                q_rot = batch.qk_norm_rope_cache_value(qt, kt, vt, qwt, kwt, key, value, qk_cfg)
+                out = batch.attention(q_rot, key.prefix(pos + 1), value.prefix(pos + 1), cfg,
+                                      mi_attn.FLASH_DECODE)
+            batch.finish()
+            names = [name for name, _ in ctx.take_kernel_profiles()]
+        finally:
+            ctx.set_kernel_profiling(False)
+        if fused:
+            want = ["attn_decode_step"] if d == 128 else ["qk_norm_rope_cache", "attn_rows"]
+            assert names[:len(want)] == want, names
+        results.append((ctx.download(out), ctx.download(key), ctx.download(value)))
+        cache.close()
+    (out_pair, key_pair, value_pair), (out_step, key_step, value_step) = results
+    # Rows other than pos are untouched; the value row is copied bit for bit.
+    others = np.ones(cap, bool)
+    others[pos] = False
+    assert (key_step[others] == k_hist[others]).all() and (value_step[others] == v_hist[others]).all()
+    assert (value_step[pos] == v[0]).all() and (value_pair[pos] == v[0]).all()
+    # The key transform sums the squares in another order: within one f16 ulp.
+    assert np.abs(key_step[pos].astype(np.int32) - key_pair[pos].astype(np.int32)).max() <= 1
+    want_q, want_k = oracle.qk_norm_rope(q, k, qw, kw, offset=pos, theta=theta, epsilon=eps)
+    kk = key_step[:pos + 1].copy()
+    ref = oracle_attention(want_q, kk, value_step[:pos + 1], hq=hq, hkv=hkv, d=d, off=pos)
+    assert_parity(out_step, ref, label=f"step {hq}/{hkv}/{d} pos {pos}")
+    assert np.abs(f16(out_step).astype(np.float64) - f16(out_pair)).max() <= TOL
+    diff = np.abs(f16(key_step[pos]).astype(np.float64) - f16(want_k[0]))
+    assert diff.max() <= max(2e-3, 2e-3 * np.abs(f16(want_k)).max())
+
+
+def test_decode_step_errors(ctx):
+    hq, hkv, d = 4, 2, 128
+    cache = ctx.kv_cache(1, hkv, d, 8)
+    key, value = cache.layer(0)
+    q, k, v = (ctx.tensor(rand(i, (1, h, d))) for i, h in ((1, hq), (2, hkv), (3, hkv)))
+    w = ctx.tensor(rand(4, (d,)))
+    batch = ctx.begin_batch()
+    with pytest.raises(mi_attn.MiError, match="query_offset must be the transform's offset"):
+        batch.decode_step_attention(q, k, v, w, w, key, value, mi_attn.QkNormRopeCacheConfig(3, 1e4, 1e-6),
+                                    mi_attn.AttentionConfig(hq, hkv, d, True, 2))
+    with pytest.raises(mi_attn.MiError, match="cache offset"):
+        batch.decode_step_attention(q, k, v, w, w, key, value, mi_attn.QkNormRopeCacheConfig(8, 1e4, 1e-6),
+                                    mi_attn.AttentionConfig(hq, hkv, d, True, 8))
+    q2 = ctx.tensor(rand(5, (2, hq, d)))
+    with pytest.raises(mi_attn.MiError):
+        batch.decode_step_attention(q2, k, v, w, w, key, value, mi_attn.QkNormRopeCacheConfig(3, 1e4, 1e-6),
+                                    mi_attn.AttentionConfig(hq, hkv, d, True, 3))
+    batch.abandon()
+    cache.close()
