@@ -244,7 +244,11 @@ def test_fused_value_append_errors(ctx):
     cache.close()
 
 
-def test_captured_fused_decode_step_replays_match_eager(ctx):
+@pytest.mark.parametrize("one_launch", [False, True])
+def test_captured_fused_decode_step_replays_match_eager(ctx, one_launch):
+    """Replays of a captured step (the two-kernel form, or
+    mi_decode_step_attention) equal the eager step bit for bit, each replay
+    after eager work of its own."""
     hq, hkv, d, cap, pos = 16, 8, 128, 1024, 600
     cache = ctx.kv_cache(1, hkv, d, cap)
     key, value = cache.layer(0)
@@ -256,6 +260,9 @@ def test_captured_fused_decode_step_replays_match_eager(ctx):
     acfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
 
     def step(batch, out=None):
+        if one_launch:
+            return batch.decode_step_attention(q_in, k_in, v_in, w, w, key, value, cfg, acfg,
+                                               out=out)
         q_rot = batch.qk_norm_rope_cache_value(q_in, k_in, v_in, w, w, key, value, cfg)
         return batch.attention(q_rot, key.prefix(pos + 1), value.prefix(pos + 1), acfg,
                                mi_attn.FLASH_DECODE, out=out)
