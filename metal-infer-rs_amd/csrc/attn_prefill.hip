@@ -26,9 +26,7 @@ namespace {
 
 using namespace mi::dev;
 
-constexpr int BM = kPrefillBlockM;  // packed rows per workgroup
 constexpr int BN = kPrefillBlockN;  // keys per KV tile
-constexpr int THREADS = 256;        // 4 waves x 32 rows
 
 // Column of key `key` (0..63 within a tile) in the transposed V tile: bits
 // 2 and 3 swapped, which is the key order of the P operand (see above).
@@ -61,9 +59,17 @@ constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 constexpr int kReadAhead = 4;
 
-template <int D>
-__global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
+// BMT packed rows per workgroup, 32 per wave: 128 (4 waves, two workgroups
+// per CU) or, for D = 128 grids of at least four workgroups per CU, 256 (8
+// waves sharing each K/V tile, one workgroup per CU).
+template <int D, int BMT>
+__global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kernel(
     const PrefillParams p) {
+  constexpr int BM = BMT;
+  constexpr int THREADS = BMT * 2;
+  constexpr int WAVES = THREADS / 64;
+  constexpr int BPW = 16 / WAVES;     // 1 KB blocks per wave of each K / V tile
+  static_assert(BM == 128 || (BM == 256 && D == 128), "row tile");
   constexpr int DC = D / 16;          // 16-wide d chunks of Q K^T
   constexpr int DT = D / 32;          // 32-row d tiles of O^T
   constexpr int KS = D + 8;           // K tile row stride (halves)
@@ -225,8 +231,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     const uint16_t *vt = vbase + (int64_t)j0 * p.v_pos;
     const int last = j0 + BN > kmax ? (int)(kmax - 1 - j0) : BN - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = wave * 4 + i;
+    for (int i = 0; i < BPW; ++i) {
+      const int blk = wave * BPW + i;
       const int row = blk * 4 + (lane >> 4);
       const int pc = lane & 15;
       const int rr = min(row, last);
@@ -422,9 +428,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_prefill_kernel(
     // bytes: float2 slot 0 = (m, l), slot 1 + 8dt + 2q + e = O values
     // (4q + 2e, 4q + 2e + 1) of d tile dt, each slot 64 lanes wide.
     constexpr uint32_t SLOTS = kPrefillPartialSlots(D);
-    const size_t split_stride = (size_t)p.row_tiles * p.kv_heads * 4 * SLOTS * 64 * 2;
+    const size_t split_stride = (size_t)p.row_tiles * p.kv_heads * WAVES * SLOTS * 64 * 2;
     float *wave_base =
-        p.partial + ((((size_t)tile * p.kv_heads + kvh) * 4 + wave) * SLOTS * 64 + lane) * 2;
+        p.partial + ((((size_t)tile * p.kv_heads + kvh) * WAVES + wave) * SLOTS * 64 + lane) * 2;
     {
       float *mine = wave_base + split * split_stride;
       store_coherent2(mine, m_run, l_total);
@@ -537,8 +543,14 @@ bool prefill_supported(uint32_t head_dim) {
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
   const dim3 grid(p.row_tiles, p.kv_heads, p.splits > 0 ? p.splits : 1);
   switch (head_dim) {
-    case 64: return dispatch(attn_prefill_kernel<64>, grid, dim3(THREADS), 0, l, p);
-    case 128: return dispatch(attn_prefill_kernel<128>, grid, dim3(THREADS), 0, l, p);
+    case 64:
+      if (p.block_m != 128) return hipErrorInvalidValue;
+      return dispatch(attn_prefill_kernel<64, 128>, grid, dim3(256), 0, l, p);
+    case 128:
+      if (p.block_m == 256)
+        return dispatch(attn_prefill_kernel<128, 256>, grid, dim3(512), 0, l, p);
+      if (p.block_m != 128) return hipErrorInvalidValue;
+      return dispatch(attn_prefill_kernel<128, 128>, grid, dim3(256), 0, l, p);
     default: return hipErrorInvalidValue;
   }
 }

@@ -135,13 +135,14 @@ struct PrefillParams {
   uint16_t *out;
   int64_t o_tok, o_head;
   uint32_t tokens, q_heads, kv_heads, group, kv_length, causal, query_offset;
-  uint32_t row_tiles;       // ceil(T * group / BLOCK_M)
+  uint32_t row_tiles;       // ceil(T * group / block_m)
+  uint32_t block_m;         // packed rows per workgroup: 128, or 256 at D = 128
   float scale_log2;
   // Split-K over keys (small grids): split z of a row tile covers key tiles
   // [z * split_tiles, (z + 1) * split_tiles); split_tiles = 0 means one split
   // per row tile. Each split of a row tile that needs several writes its
   // unnormalised rows (m, l, O[D]) as f32 to `partial`, laid out
-  // [splits][row_tiles][kv_heads][4 waves][kPrefillPartialSlots(D)][64 lanes]
+  // [splits][row_tiles][kv_heads][block_m / 32 waves][kPrefillPartialSlots(D)][64 lanes]
   // float2, then counts its arrival in counters[tile * kv_heads + kv_head];
   // the last split to arrive merges all of them in split order and resets
   // the counter to zero.
@@ -236,6 +237,7 @@ hipError_t launch_matvec(const MatvecParams &p, const Launch &l);
 // Rows of the packed (token, head-in-group) M dimension per prefill
 // workgroup, and keys per KV tile.
 constexpr uint32_t kPrefillBlockM = 128;
+constexpr uint32_t kPrefillBlockM2 = 256;  // large D = 128 grids
 constexpr uint32_t kPrefillBlockN = 64;
 // Most key splits of one prefill row tile.
 constexpr uint32_t kMaxPrefillSplits = 8;

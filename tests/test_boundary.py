@@ -224,10 +224,15 @@ def test_flash_prefill_routes_to_mfma_kernel():
         q, k = tensor((2048, 16, d)), tensor((2048, 8, d))
         p = plan(q, k, k, AttentionConfig(16, 8, d, True, 0), FLASH_PREFILL)
         assert p["kernel"] == expected, d
-    # c5: 4096 tokens x 8 heads per KV head = 256 row tiles of 128, one per KV head
+    # c5: 4096 tokens x 8 heads per KV head = 128 row tiles of 256 (8 waves),
+    # 1024 workgroups: at least four per CU
     q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
-    assert p["kernel"] == "attn_prefill" and p["grid"][:2] == (256, 8)
+    assert p["kernel"] == "attn_prefill" and p["grid"][:2] == (128, 8) and p["block_threads"] == 512
+    # half of c5's rows: 512 such workgroups, so 128-row tiles
+    q = tensor((2048, 64, 128))
+    p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
+    assert p["grid"][:2] == (128, 8) and p["block_threads"] == 256
     # c3: 2048 x 2 = 4096 packed rows -> 32 row tiles per KV head
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     assert plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)["grid"][:2] == (32, 8)

@@ -130,6 +130,29 @@ def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
         assert_parity(out, ref, label=f"T={T} off={off} causal={causal}")
 
 
+@pytest.mark.parametrize("hq,hkv,T,off,causal", [
+    (64, 8, 4100, 3, True),      # ragged last row tile, GQA 8
+    (8, 8, 33000, 0, True),      # MHA: a row tile spans 256 tokens
+    (32, 8, 8200, 0, False)])
+def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
+    """Grids of at least four 256-row workgroups per CU run the 8-wave row
+    tile; checked on 48 rows (first, last, seeded sample) against the oracle."""
+    rng = np.random.default_rng(T + hq)
+    L = off + T if causal else T + 40
+    q = rng.standard_normal((T, hq, 128)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, 128)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, 128)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=128, off=off)
+    info = ctx.plan(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v),
+                    mi_attn.AttentionConfig(hq, hkv, 128, causal, off), mi_attn.FLASH_PREFILL)
+    assert info["kernel"] == "attn_prefill" and info["block_threads"] == 512, info
+    out = run_attention(ctx, q, k, v, kind="flash-prefill", causal=causal, **geo)
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(T - 16, T),
+                                     rng.choice(T, 16, replace=False)]))
+    ref = oracle_attention(q, k, v, causal=causal, rows=rows, **geo)
+    assert_parity(out[rows], ref, label=f"T={T} hq={hq}")
+
+
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("hq,hkv,T,off,causal", [
     (8, 8, 700, 37, True), (16, 8, 1000, 300, True), (64, 8, 520, 37, True),
