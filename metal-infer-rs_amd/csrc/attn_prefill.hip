@@ -225,11 +225,32 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
   // Direct loads of tile `ti` into LDS stage `stage`: each wave fills four
   // 1 KB blocks, lane L writing bytes 16L..16L+15 of a block, so the lane
   // fetches the global 16 bytes that belong at that swizzled position.
+  // Full tiles: loop-invariant per-lane byte offsets from a wave-uniform
+  // tile base (scalar base + 32-bit vector offset per load).
+  uint32_t k_off[BPW], v_off[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int row = (wave * BPW + i) * 4 + (lane >> 4), pc = lane & 15;
+    k_off[i] = (uint32_t)(row * p.k_pos + ((pc ^ (row & 15)) * 8)) * 2u;
+    v_off[i] = (uint32_t)(row * p.v_pos + ((pc ^ ((row & 3) << 2)) * 8)) * 2u;
+  }
   auto issue_tile = [&](uint32_t ti, int stage) {
     const uint32_t j0 = ti * BN;
     const uint16_t *kt = kbase + (int64_t)j0 * p.k_pos;
     const uint16_t *vt = vbase + (int64_t)j0 * p.v_pos;
-    const int last = j0 + BN > kmax ? (int)(kmax - 1 - j0) : BN - 1;
+    if (j0 + BN <= kmax) {
+#pragma unroll
+      for (int i = 0; i < BPW; ++i) {
+        const int blk = wave * BPW + i;
+        load_lds16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(kt) + k_off[i]),
+                   k_stage(stage) + blk * 512);
+        load_lds16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(vt) + v_off[i]),
+                   v_stage(stage) + blk * 512);
+      }
+      return;
+    }
+    // Partial last tile: rows past the last key re-read that key.
+    const int last = (int)(kmax - 1 - j0);
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
       const int blk = wave * BPW + i;

@@ -237,7 +237,10 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
   }
   if (kind == MI_ATTN_FLASH_PREFILL && kernels::prefill_supported(p.D) &&
       vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8) &&
-      (out == nullptr || vector_friendly(*out, 4)) && (uint64_t)p.T * p.G < (1ull << 31)) {
+      (out == nullptr || vector_friendly(*out, 4)) && (uint64_t)p.T * p.G < (1ull << 31) &&
+      // A key tile's 32-bit byte offsets (64 rows) stay below 2^32.
+      (uint64_t)std::max(k->stride[0], v->stride[0]) * kernels::kPrefillBlockN * 2 + 512 <
+          (1ull << 32)) {
     p.family = Family::Prefill;
     p.kernel = "attn_prefill";
     p.threads = 256;
