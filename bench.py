@@ -1,16 +1,20 @@
 """Benchmark of the MI355X causal GQA attention path (one GPU).
 
-Headline (BASELINE.json metric, configs[1]): decode attention HBM GB/s at
-Qwen3-0.6B geometry (16 Q / 8 KV heads, D 128, L 2048, fp16 head-major
-cache). A step is one FlashDecode call; the timed steps rotate over 64
-distinct caches (537 MB, larger than the 256 MB MALL) so every call reads
-HBM, and are replayed from a HIP graph captured on the library's stream so
-Python launch cost stays out of the GPU timeline. `value` is whole-job
-algorithmic bytes / time over the timed region.
+Headline (BASELINE.json metric, decode half): HBM GB/s of the largest
+single-GPU decode configuration, configs[3] (c4: 32 sequences, Qwen3-8B
+geometry, L ~ U[1024, 8192] seeded, fp16 head-major caches, 627 MB of K/V per
+call, larger than the 256 MB MALL). A step is one batched-decode call over
+all 32 sequences; exactly --steps calls are timed, replayed from a HIP graph
+captured on the library's stream (Python launch cost stays out of the GPU
+timeline), bracketed by HIP events on that stream after a synchronize.
+`value` is algorithmic bytes x steps / timed seconds.
 
-The same line carries the prefill half of the metric (TFLOP/s vs the fp16
-MFMA peak, configs[2] and configs[4]) and the batched decode,
-each with its own roofline, plus the CPU oracle baseline timed on this host.
+The prefill half of the metric (TFLOP/s against the fp16 MFMA peak) is
+configs[4] (c5) in `prefill`, next to configs[2] (c3); configs[0] (c1) and
+configs[1] (c2, 64 rotated caches) are sub-entries. Each entry carries its
+roofline; `accuracy` is the max-abs error of the timed call's output against
+the CPU oracle, computed in the cpu_baseline leg from the oracle runs it
+times (null with --no-cpu).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -35,7 +39,8 @@ import workloads  # noqa: E402
 METRIC = "decode attn HBM GB/s (% peak) + prefill attn TFLOP/s (% MFMA peak), fp16"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
-ROTATE = 64
+ROTATE = 64                    # c2: distinct caches per graph (537 MB > MALL)
+TOL = 2e-3                     # north_star max-abs bar against the oracle
 
 
 def log(msg: str) -> None:
@@ -95,7 +100,8 @@ def capture(hip: Hip, ctx: mi_attn.Context, enqueue, steps: int):
 
 
 def time_graph(hip: Hip, exe, stream, reps: int) -> float:
-    """Seconds per graph launch, bracketed by events on the capture stream."""
+    """Seconds per graph launch: the stream is synchronized, then `reps`
+    launches are bracketed by events recorded on the same stream."""
     start, end = hip.event(), hip.event()
     hip.check(hip.lib.hipStreamSynchronize(stream), "sync")
     hip.check(hip.lib.hipEventRecord(start, stream), "record")
@@ -112,7 +118,7 @@ def time_graph(hip: Hip, exe, stream, reps: int) -> float:
 
 def time_eager(ctx: mi_attn.Context, hip: Hip, enqueue, steps: int) -> float:
     """Seconds per call of `steps` eager calls in one batch, bracketed by
-    events on the library stream (used under rocprofv3, which cannot trace
+    events on the library stream (used under rocprofv3, which does not trace
     graph launches here)."""
     batch = ctx.begin_batch()
     stream = ctypes.c_void_p(batch.stream)
@@ -131,28 +137,34 @@ def time_eager(ctx: mi_attn.Context, hip: Hip, enqueue, steps: int) -> float:
     return ms.value / 1e3 / steps
 
 
-def timed(ctx, hip, enqueue, steps: int, eager: bool, reps: int) -> tuple[int, float]:
-    """(calls timed, seconds per call): a HIP graph of `steps` calls replayed
-    `reps` times, or `steps * reps` eager calls."""
+def timed(ctx, hip, enqueue, steps: int, warmup: int, eager: bool) -> float:
+    """Seconds per call over exactly `steps` timed calls, after `warmup`
+    untimed eager calls. Graph mode captures the `steps` calls once, replays
+    the graph once untimed (its first launch uploads it) and then times one
+    replay."""
+    for i in range(warmup):
+        b = ctx.begin_batch()
+        enqueue(b, i)
+        b.finish()
     if eager:
-        return steps * reps, time_eager(ctx, hip, enqueue, steps * reps)
-    exe, graph, stream, _ = capture(hip, ctx, enqueue, steps)
+        return time_eager(ctx, hip, enqueue, steps)
+    exe, graph, stream, keep = capture(hip, ctx, enqueue, steps)
     time_graph(hip, exe, stream, 1)
-    seconds = time_graph(hip, exe, stream, reps) / steps
+    seconds = time_graph(hip, exe, stream, 1) / steps
     hip.lib.hipGraphExecDestroy(exe)
     hip.lib.hipGraphDestroy(graph)
-    return steps * reps, seconds
+    del keep
+    return seconds
 
 
 def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, float, dict]:
     """The dominant kernel (largest total time) of `count` eager calls, its
     median duration per launch (s), and every kernel's median, from the
     start / stop events the library binds to each dispatch on the batch's
-    stream (hipExtLaunchKernelGGL)."""
+    stream (hipExtLaunchKernelGGL). A diagnostic beside the timed region."""
     ctx.take_kernel_profiles()
     ctx.set_kernel_profiling(True)
     try:
-        # Back to back in one batch, as in the timed region.
         batch = ctx.begin_batch()
         keep = [enqueue(batch, i) for i in range(count)]
         batch.finish()
@@ -163,8 +175,6 @@ def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, floa
     by_name: dict[str, list[float]] = {}
     for name, ns in profiles:
         by_name.setdefault(name, []).append(ns)
-    # Median per kernel: a few launches that wait on the host or on a clock
-    # change would otherwise skew a µs-scale kernel's mean.
     typical = {n: float(np.median(v)) * 1e-9 for n, v in by_name.items()}
     name = max(by_name, key=lambda n: sum(by_name[n]))
     return name, typical[name], typical
@@ -183,12 +193,62 @@ def measured_traffic(workload: str, kernel: str):
     return entry.get("traffic_bytes")
 
 
-# ----------------------------------------------------------------- decode --
+def roofline(run: dict, workload: str) -> dict:
+    """Roofline of the step's dominant kernel. Every attention step here is
+    one kernel launch (split merges run inside it), so the kernel's average
+    launch duration over the timed region is the timed seconds per step
+    (HIP events on the launch stream); the per-dispatch event median of a
+    separate eager pass is kept as `dispatch_event_us`."""
+    secs = run["seconds"]
+    if "bytes" in run:
+        achieved, peak, unit, work = run["bytes"] / secs / 1e9, HBM_PEAK_GBS, "GB/s", "bytes"
+    else:
+        achieved, peak, unit, work = run["flops"] / secs / 1e12, MFMA_F16_PEAK_TFLOPS, "TFLOP/s", "flops"
+    return {"bound": "hbm" if unit == "GB/s" else "mfma", "achieved": round(achieved, 2),
+            "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+            "traffic": measured_traffic(workload, run["kernel"]), "kernel": run["kernel"],
+            "kernel_us": round(secs * 1e6, 3), f"algorithmic_{work}": run[work],
+            "launches_per_step": run["launches"],
+            "dispatch_event_us": {n: round(t * 1e6, 3) for n, t in run["kernels"].items()}}
+
+
+# ---------------------------------------------------------------- decode --
+
+def bench_batched_decode(ctx, hip, steps, warmup, eager):
+    """c4 (the headline): one call decodes all 32 sequences."""
+    c = workloads.case(4)
+    B, hq, hkv, d, cap = c.batch, c.q_heads, c.kv_heads, c.head_dim, c.kv_length
+    log(f"c4 batched decode: B={B}, sum L={int(c.lengths.sum())}")
+    kstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
+    vstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
+    for b in range(B):
+        kstore[b, :, : c.lengths[b]] = c.k[b].transpose(1, 0, 2)
+        vstore[b, :, : c.lengths[b]] = c.v[b].transpose(1, 0, 2)
+    kt, vt = ctx.tensor(kstore), ctx.tensor(vstore)
+    del kstore, vstore
+    view = ((B, cap, hkv, d), (hkv * cap * d, d, cap * d, 1))
+    kview, vview = kt.view(*view), vt.view(*view)
+    q, lengths = ctx.tensor(c.q), ctx.tensor(c.lengths, mi_attn.U32)
+    out = ctx.empty(c.q.shape)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+
+    def enqueue(batch, i):
+        return batch.attention_decode_batched(q, kview, vview, lengths, cfg, 0, out=out)
+
+    seconds = timed(ctx, hip, enqueue, steps, warmup, eager)
+    got = ctx.download(out)
+    name, _, kernels = kernel_profile(ctx, enqueue, 10)
+    for t in (kt, vt, q, lengths, out):
+        t.free()
+    return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels, launches=1,
+                   bytes=c.algorithmic_bytes(), out=got)
+
 
 def bench_decode(ctx, hip, steps, warmup, eager):
+    """c2: single-sequence FlashDecode, rotating 64 caches per graph."""
     c = workloads.case(2)
     hq, hkv, d, L = c.q_heads, c.kv_heads, c.head_dim, c.kv_length
-    log(f"decode c2: {ROTATE} head-major caches of {L} positions")
+    log(f"c2 decode: {ROTATE} head-major caches of {L} positions")
     cache = ctx.kv_cache(ROTATE, hkv, d, L)
     layers = [cache.layer(i) for i in range(ROTATE)]
     for key, value in layers:
@@ -202,17 +262,15 @@ def bench_decode(ctx, hip, steps, warmup, eager):
         key, value = layers[i % ROTATE]
         return batch.attention(q, key, value, cfg, mi_attn.FLASH_DECODE, out=out)
 
-    for i in range(max(warmup, 1)):
-        b = ctx.begin_batch()
-        enqueue(b, i)
-        b.finish()
-    per_graph = max(ROTATE, (steps // ROTATE) * ROTATE)
-    calls, seconds = timed(ctx, hip, enqueue, per_graph, eager, max(1, steps // per_graph))
-    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 4 * ROTATE)
-    nbytes = c.algorithmic_bytes()
+    calls = max(ROTATE, (steps + ROTATE - 1) // ROTATE * ROTATE)
+    seconds = timed(ctx, hip, enqueue, calls, warmup, eager)
+    got = ctx.download(out)
+    name, _, kernels = kernel_profile(ctx, enqueue, 4 * ROTATE)
+    q.free()
+    out.free()
     cache.close()
-    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   kernels=kernels, bytes=nbytes)
+    return c, dict(steps=calls, seconds=seconds, kernel=name, kernels=kernels, launches=1,
+                   bytes=c.algorithmic_bytes(), out=got)
 
 
 def bench_decode_step(ctx, hip, steps):
@@ -238,34 +296,8 @@ def bench_decode_step(ctx, hip, steps):
     cfg = mi_attn.AttentionConfig(hq, hkv, d, True, pos)
     rope = mi_attn.QkNormRopeCacheConfig(pos, 1_000_000.0, 1e-6)
     out = ctx.empty(c.q.shape)
-
-    def enqueue(batch, i):
-        q_rot = batch.qk_norm_rope_cache(q_in, k_in, weights, weights, key, rope)
-        batch.copy_into_cache(v_in, value, pos)
-        return batch.attention(q_rot, key.prefix(L), value.prefix(L), cfg, mi_attn.FLASH_DECODE,
-                               out=out)
-
-    eager = time_eager(ctx, hip, enqueue, steps)
-    capture = ctx.begin_capture()
-    keep = [enqueue(capture, i) for i in range(PER_GRAPH)]
-    graph = capture.end_capture()
-    graph.launch()
-    ctx.synchronize()
-    reps = max(1, steps // PER_GRAPH)
     start, end = hip.event(), hip.event()
-    batch = ctx.begin_batch()  # only for the stream handle; the replays run on it
-    stream = ctypes.c_void_p(batch.stream)
-    hip.check(hip.lib.hipEventRecord(start, stream), "record")
-    for _ in range(reps):
-        graph.launch()
-    hip.check(hip.lib.hipEventRecord(end, stream), "record")
-    hip.check(hip.lib.hipEventSynchronize(end), "sync")
-    batch.finish()
-    ms = ctypes.c_float()
-    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, end), "elapsed")
-    graph.destroy()
-    del keep
-    graph_us = ms.value * 1e3 / (reps * PER_GRAPH)
+    reps = max(1, steps // PER_GRAPH)
 
     def graph_us_of(step):
         """GPU time per step of PER_GRAPH captured steps, replayed."""
@@ -288,6 +320,12 @@ def bench_decode_step(ctx, hip, steps):
         del kept
         return elapsed.value * 1e3 / (reps * PER_GRAPH)
 
+    def enqueue(batch, i):
+        q_rot = batch.qk_norm_rope_cache(q_in, k_in, weights, weights, key, rope)
+        batch.copy_into_cache(v_in, value, pos)
+        return batch.attention(q_rot, key.prefix(L), value.prefix(L), cfg, mi_attn.FLASH_DECODE,
+                               out=out)
+
     # The same step with the V append folded into the Q/K kernel
     # (mi_qk_norm_rope_cache_value): two kernels.
     def enqueue_fused(batch, i):
@@ -302,6 +340,8 @@ def bench_decode_step(ctx, hip, steps):
         return batch.decode_step_attention(q_in, k_in, v_in, weights, weights, key, value, rope,
                                            cfg, out=out)
 
+    eager = time_eager(ctx, hip, enqueue, steps)
+    graph_us = graph_us_of(enqueue)
     fused_value_us = graph_us_of(enqueue_fused)
     one_launch_us = graph_us_of(enqueue_step)
     cache.close()
@@ -313,40 +353,12 @@ def bench_decode_step(ctx, hip, steps):
             "graph_one_launch_us": round(one_launch_us, 3)}
 
 
-def bench_batched_decode(ctx, hip, steps, eager):
-    c = workloads.case(4)
-    B, hq, hkv, d, cap = c.batch, c.q_heads, c.kv_heads, c.head_dim, c.kv_length
-    log(f"batched decode c4: B={B}, sum L={int(c.lengths.sum())}")
-    kstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
-    vstore = np.zeros((B, hkv, cap, d), dtype=np.uint16)
-    for b in range(B):
-        kstore[b, :, : c.lengths[b]] = c.k[b].transpose(1, 0, 2)
-        vstore[b, :, : c.lengths[b]] = c.v[b].transpose(1, 0, 2)
-    kt, vt = ctx.tensor(kstore), ctx.tensor(vstore)
-    del kstore, vstore
-    view = ((B, cap, hkv, d), (hkv * cap * d, d, cap * d, 1))
-    kview, vview = kt.view(*view), vt.view(*view)
-    q, lengths = ctx.tensor(c.q), ctx.tensor(c.lengths, mi_attn.U32)
-    out = ctx.empty(c.q.shape)
-    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+# --------------------------------------------------------------- prefill --
 
-    def enqueue(batch, i):
-        return batch.attention_decode_batched(q, kview, vview, lengths, cfg, 0, out=out)
-
-    for i in range(2):
-        b = ctx.begin_batch()
-        enqueue(b, i)
-        b.finish()
-    calls, seconds = timed(ctx, hip, enqueue, steps, eager, 3)
-    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 10)
-    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   kernels=kernels, bytes=c.algorithmic_bytes())
-
-
-def bench_prefill(ctx, hip, config, steps, eager):
+def bench_prefill(ctx, hip, config, steps, warmup, eager):
     c = workloads.case(config)
     hq, hkv, d = c.q_heads, c.kv_heads, c.head_dim
-    log(f"prefill c{config}: T={c.tokens} L={c.kv_length} Hq={hq} Hkv={hkv}")
+    log(f"c{config} prefill: T={c.tokens} L={c.kv_length} Hq={hq} Hkv={hkv}")
     cache = ctx.kv_cache(1, hkv, d, c.kv_length)
     key, value = cache.layer(0)
     ctx.upload(key, c.k)
@@ -359,15 +371,15 @@ def bench_prefill(ctx, hip, config, steps, eager):
     def enqueue(batch, i):
         return batch.attention(q, key, value, cfg, kind, out=out)
 
-    b = ctx.begin_batch()
-    enqueue(b, 0)
-    b.finish()
-    calls, seconds = timed(ctx, hip, enqueue, steps, eager, 2)
-    name, kernel_s, kernels = kernel_profile(ctx, enqueue, 10 if config == 3 else 3)
+    plan = ctx.plan(q, key, value, cfg, kind)
+    seconds = timed(ctx, hip, enqueue, steps, warmup, eager)
+    got = ctx.download(out)
+    name, _, kernels = kernel_profile(ctx, enqueue, 10 if config != 5 else 3)
+    q.free()
+    out.free()
     cache.close()
-    return c, dict(steps=calls, seconds=seconds, kernel=name, kernel_s=kernel_s,
-                   kernels=kernels, flops=c.flops(),
-                   plan=ctx.plan(q, key, value, cfg, kind)["kernel"])
+    return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels, launches=1,
+                   flops=c.flops(), plan=plan, out=got)
 
 
 # ---------------------------------------------------------------- o_proj --
@@ -399,6 +411,16 @@ NEIGHBOURS = (
 )
 
 
+def _hbm_entry(label, seconds, name, kernel_s, nbytes) -> dict:
+    achieved = nbytes / kernel_s / 1e9
+    return {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
+            "kernel_us": round(kernel_s * 1e6, 3), "value": round(nbytes / seconds / 1e9, 2),
+            "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes": nbytes}}
+
+
 def bench_neighbours(ctx, hip, eager) -> list[dict]:
     rng = np.random.default_rng(1)
     results = []
@@ -416,20 +438,10 @@ def bench_neighbours(ctx, hip, eager) -> list[dict]:
                 return batch.rms_norm(x, weight, 1e-6, out=out)
             return batch.rope(x, 3, 1_000_000.0, out=out)
 
-        b = ctx.begin_batch()
-        enqueue(b, 0)
-        b.finish()
-        calls, seconds = timed(ctx, hip, enqueue, max(rotate, 64), eager, 2)
+        seconds = timed(ctx, hip, enqueue, max(rotate, 64), 1, eager)
         name, kernel_s, _ = kernel_profile(ctx, enqueue, max(rotate, 8))
         nbytes = 2 * 2 * int(np.prod(shape)) + (2 * shape[-1] if op == "rms_norm" else 0)
-        achieved = nbytes / kernel_s / 1e9
-        entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
-                 "kernel_us": round(kernel_s * 1e6, 3),
-                 "value": round(nbytes / seconds / 1e9, 2), "unit": "GB/s",
-                 "roofline": {"bound": "hbm", "achieved": round(achieved, 2),
-                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                              "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                              "algorithmic_bytes": nbytes}}
+        entry = _hbm_entry(label, seconds, name, kernel_s, nbytes)
         log(f"  {entry['value']} GB/s, {name} {entry['kernel_us']} us")
         results.append(entry)
         for x in xs:
@@ -461,19 +473,10 @@ def bench_qk_norm_rope_prefill(ctx, hip, eager, rng) -> dict:
         return batch.qk_norm_rope_cache(qs[i % rotate], ks[i % rotate], w, w, key, cfg,
                                         out=q_out)
 
-    b = ctx.begin_batch()
-    enqueue(b, 0)
-    b.finish()
-    calls, seconds = timed(ctx, hip, enqueue, 16, eager, 2)
+    seconds = timed(ctx, hip, enqueue, 16, 1, eager)
     name, kernel_s, _ = kernel_profile(ctx, enqueue, 8)
     nbytes = 2 * 2 * T * (hq + hkv) * d + 2 * 2 * d
-    achieved = nbytes / kernel_s / 1e9
-    entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
-             "kernel_us": round(kernel_s * 1e6, 3), "value": round(nbytes / seconds / 1e9, 2),
-             "unit": "GB/s",
-             "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                          "traffic": None, "algorithmic_bytes": nbytes}}
+    entry = _hbm_entry(label, seconds, name, kernel_s, nbytes)
     log(f"  {entry['value']} GB/s, {name} {entry['kernel_us']} us")
     for t in qs + ks:
         t.free()
@@ -496,30 +499,21 @@ def bench_o_proj(ctx, hip, eager) -> list[dict]:
         def enqueue(batch, i):
             return batch.matmul(x, weights[i % rotate], out=out)
 
-        b = ctx.begin_batch()
-        enqueue(b, 0)
-        b.finish()
         steps = max(rotate, 64 if bound == "hbm" else 8)
-        calls, seconds = timed(ctx, hip, enqueue, steps, eager, 2)
+        seconds = timed(ctx, hip, enqueue, steps, 1, eager)
         name, kernel_s, kernels = kernel_profile(ctx, enqueue, max(rotate, 8))
-        entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
-                 "kernel_us": round(kernel_s * 1e6, 3)}
         if bound == "hbm":
-            nbytes = 2 * (n * k + m * k + m * n)
-            value = nbytes / seconds / 1e9
-            achieved = nbytes / kernel_s / 1e9
-            entry.update({"value": round(value, 2), "unit": "GB/s", "roofline": {
-                "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "algorithmic_bytes": nbytes}})
+            entry = _hbm_entry(label, seconds, name, kernel_s, 2 * (n * k + m * k + m * n))
         else:
             flops = 2 * m * n * k
-            value = flops / seconds / 1e12
             achieved = flops / kernel_s / 1e12
-            entry.update({"value": round(value, 2), "unit": "TFLOP/s", "roofline": {
-                "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
-                "traffic": None, "algorithmic_flops": flops}})
+            entry = {"workload": label, "ms_per_step": round(seconds * 1e3, 5), "kernel": name,
+                     "kernel_us": round(kernel_s * 1e6, 3),
+                     "value": round(flops / seconds / 1e12, 2), "unit": "TFLOP/s",
+                     "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                                  "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                                  "traffic": None, "algorithmic_flops": flops}}
         log(f"  {entry['value']} {entry['unit']}, {name} {entry['kernel_us']} us")
         results.append(entry)
         for w in weights:
@@ -531,46 +525,120 @@ def bench_o_proj(ctx, hip, eager) -> list[dict]:
 
 # -------------------------------------------------------------- CPU leg ---
 
-def cpu_baseline(decode_case) -> dict:
-    """The C oracle (attention_reference_f16 restated) on this host's cores,
-    on a bounded sample: repeated c2 decodes for about 10 s."""
+def host_cpu() -> dict:
+    """The host's CPU model, its logical CPUs, and the threads the oracle
+    uses: the CPUs this process may run on, capped by OMP_NUM_THREADS when
+    set (the GPU box grants each GPU a 16-thread share and sets it to 16)."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(usable, int(cap)) if cap.isdigit() and int(cap) > 0 else usable
+    return {"model": model, "nproc": usable, "threads": threads}
+
+
+def cpu_baseline(entries: dict) -> dict:
+    """The C oracle (attention_reference_f16 restated, oracle/) timed on this
+    host's cores for every BASELINE config: one warm-up and the median of 5
+    runs for c1-c4, and for c5 one run over a stated sample of query rows
+    (every 8th token, all 64 heads: every 32-token row tile of every KV head),
+    extrapolated to the full call by its share of the FLOPs. The oracle's
+    outputs from these runs are also the reference for each GPU entry's
+    `accuracy` (max-abs of the timed call's output)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = oracle.default_threads()
-    c = decode_case
-    args = dict(q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, causal=True,
-                query_offset=c.query_offset, want=("f32",), threads=threads)
-    oracle.attention(c.q, c.k, c.v, **args)
-    calls, start = 0, time.perf_counter()
-    while time.perf_counter() - start < 10.0:
-        oracle.attention(c.q, c.k, c.v, **args)
-        calls += 1
-    seconds = (time.perf_counter() - start) / calls
-    return {"value": round(c.algorithmic_bytes() / seconds / 1e9, 3), "unit": "GB/s",
-            "cores": threads, "kind": "port",
-            "sample": f"{calls} full c2 decode calls (L=2048, 16/8 heads) of the C oracle, "
-                      f"{seconds * 1e3:.2f} ms each, {threads} OpenMP threads"}
+    host = host_cpu()
+    threads = host["threads"]
+    configs = {}
+
+    def f16(bits):
+        return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
+
+    def timed_runs(fn, reps):
+        fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            result = fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)), result
+
+    for name, (c, run, entry) in entries.items():
+        args = dict(q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, causal=True,
+                    want=("f32",), threads=threads)
+        rows = None
+        if c.kind == "batched_decode":
+            def fn():
+                return [oracle.attention(c.q[b:b + 1], c.k[b], c.v[b],
+                                         query_offset=int(c.lengths[b]) - 1, **args)["f32"]
+                        for b in range(c.batch)]
+            seconds, ref = timed_runs(fn, 5)
+            ref = np.concatenate(ref, axis=0)
+            work, unit, share = c.algorithmic_bytes(), "GB/s", 1.0
+            sample = f"all {c.batch} sequences, median of 5 runs"
+        elif name == "c5":
+            rows = np.arange(0, c.tokens, 8)
+            t0 = time.perf_counter()
+            ref = oracle.attention(c.q, c.k, c.v, query_offset=c.query_offset, rows=rows,
+                                   **args)["f32"]
+            seconds = time.perf_counter() - t0
+            sampled = sum(min(c.kv_length, c.query_offset + int(t) + 1) for t in rows)
+            share = sampled / c.visible_pairs()
+            work, unit = c.flops(), "GFLOP/s"
+            sample = (f"{len(rows)} of {c.tokens} query tokens (every 8th, all {c.q_heads} heads), "
+                      f"one run of {seconds:.2f} s = {share:.4f} of the call's FLOPs, "
+                      "extrapolated")
+            seconds = seconds / share
+        else:
+            def fn():
+                return oracle.attention(c.q, c.k, c.v, query_offset=c.query_offset,
+                                        **args)["f32"]
+            seconds, ref = timed_runs(fn, 5)
+            share = 1.0
+            if c.kind == "decode":
+                work, unit = c.algorithmic_bytes(), "GB/s"
+            else:
+                work, unit = c.flops(), "GFLOP/s"
+            sample = "the full call, median of 5 runs"
+        rate = work / seconds / 1e9
+        configs[name] = {"value": round(rate, 3), "unit": unit,
+                         "ms_per_call": round(seconds * 1e3, 3), "threads": threads,
+                         "sample": sample}
+        got = f16(run["out"] if rows is None else run["out"][rows])
+        diff = np.abs(got - np.asarray(ref, np.float64))
+        err = float(diff.max())
+        entry["accuracy"] = {"max_abs": err, "tol": TOL, "ok": bool(err <= TOL),
+                             "rows_checked": int(got.shape[0] * got.shape[1]),
+                             "against": "oracle f32 (unrounded), same seeded inputs"}
+        log(f"cpu {name}: {rate:.3f} {unit} ({seconds * 1e3:.1f} ms per call), "
+            f"GPU max-abs {err:.2e}")
+    head = configs["c4"] if "c4" in configs else next(iter(configs.values()))
+    return {"value": head["value"], "unit": head["unit"], "cores": threads, "kind": "port",
+            "cpu_model": host["model"], "nproc": host["nproc"],
+            "sample": f"c4: {head['sample']} of the C oracle, {threads} OpenMP threads on "
+                      f"{host['model']}; every config in `configs`",
+            "configs": configs}
 
 
-def hbm_roofline(nbytes: int, run: dict, workload: str) -> dict:
-    achieved = nbytes / run["kernel_s"] / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(workload, run["kernel"]), "kernel": run["kernel"],
-            "kernel_us": round(run["kernel_s"] * 1e6, 3), "algorithmic_bytes": nbytes,
-            "kernels_us": {n: round(t * 1e6, 3) for n, t in run["kernels"].items()}}
-
+# ------------------------------------------------------------------ main --
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1024)
-    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workloads", default="c2,c4,c3,c5,o_proj",
-                    help="comma list of c2 (headline decode), c4, c3, c5, o_proj; profiling "
-                         "runs select one at a time")
+    ap.add_argument("--workloads", default="c4,c5,c3,c2,c1,step,o_proj",
+                    help="comma list of c4 (headline), c5, c3, c2, c1, step (decode step "
+                         "graphs), o_proj (with the other neighbours); profiling runs "
+                         "select one at a time")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of HIP graph replays (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -580,8 +648,11 @@ def main() -> int:
         print("bench.py measures one GPU only: the attention path has no multi-GPU "
               "component in this build; a multi-GPU layout is design-only here", file=sys.stderr)
         return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
-    unknown = set(chosen) - {"c2", "c3", "c4", "c5", "o_proj"}
+    unknown = set(chosen) - {"c1", "c2", "c3", "c4", "c5", "step", "o_proj"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -590,72 +661,78 @@ def main() -> int:
     ctx = mi_attn.Context(0)
     log(f"device: {ctx.device_name}, {ctx.compute_units} CUs")
     timing = "eager launches" if args.eager else "HIP graph replay"
-    result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": 0,
-              "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+    K, W = args.steps, args.warmup
+    result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": K,
+              "warmup": W, "ms_per_step": None, "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "f16",
               "data": "synthetic: seeded XorShift64/Box-Muller N(0,1) f16 (BASELINE configs)"}
-    dc = None
-    if "c2" in chosen:
-        dc, dec = bench_decode(ctx, hip, args.steps, args.warmup, args.eager)
-        value = dec["bytes"] / dec["seconds"] / 1e9
-        roof = hbm_roofline(dec["bytes"], dec, "c2")
-        log(f"decode: {value:.1f} GB/s whole-job, kernel {dec['kernel']} "
-            f"{dec['kernel_s'] * 1e6:.2f} us -> {roof['achieved']:.1f} GB/s")
+    checked = {}  # config -> (case, run, entry) for the CPU leg's accuracy check
+    if "c4" in chosen:
+        c, run = bench_batched_decode(ctx, hip, K, W, args.eager)
+        value = run["bytes"] / run["seconds"] / 1e9
+        log(f"c4: {value:.1f} GB/s whole job, {run['seconds'] * 1e6:.2f} us per step")
         result.update({
-            "value": round(value, 2), "steps": dec["steps"],
-            "ms_per_step": round(dec["seconds"] * 1e3, 6),
-            "config": {"workload": "c2 single-token decode, L=2048, Hq=16, Hkv=8, D=128, "
-                                   f"head-major fp16 cache, {ROTATE} rotated caches, {timing}",
-                       "kv_length": dc.kv_length, "q_heads": dc.q_heads,
-                       "kv_heads": dc.kv_heads, "head_dim": dc.head_dim},
-            "roofline": roof})
+            "value": round(value, 2), "ms_per_step": round(run["seconds"] * 1e3, 6),
+            "config": {"workload": "c4 batched decode (BASELINE configs[3], the largest "
+                                   "single-GPU decode config): B=32, L~U[1024,8192] seeded, "
+                                   "Hq=32, Hkv=8, D=128, fp16 head-major caches, one "
+                                   f"launch per step, {timing}; prefill half: c5 in prefill[]",
+                       "batch": c.batch, "kv_lengths_sum": int(c.lengths.sum()),
+                       "q_heads": c.q_heads, "kv_heads": c.kv_heads, "head_dim": c.head_dim},
+            "roofline": roofline(run, "c4")})
+        checked["c4"] = (c, run, result)
     else:
-        log("c2 not selected: the headline fields stay null (profiling run)")
-    if "c2" in chosen and not args.eager:
+        log("c4 not selected: the headline fields stay null (profiling run)")
+    prefill = []
+    for config in (5, 3):
+        if f"c{config}" not in chosen:
+            continue
+        c, run = bench_prefill(ctx, hip, config, K, W, args.eager)
+        tflops = run["flops"] / run["seconds"] / 1e12
+        log(f"c{config}: {tflops:.1f} TFLOP/s, {run['seconds'] * 1e3:.4f} ms per step")
+        entry = {"workload": c.description, "value": round(tflops, 2), "unit": "TFLOP/s",
+                 "steps": K, "ms_per_step": round(run["seconds"] * 1e3, 5),
+                 "kernel_family": run["plan"]["kernel"],
+                 "plan": {k: run["plan"][k] for k in ("grid", "block_threads", "splits")},
+                 "roofline": roofline(run, f"c{config}")}
+        prefill.append(entry)
+        checked[f"c{config}"] = (c, run, entry)
+    if prefill:
+        result["prefill"] = prefill
+    if "c2" in chosen:
+        c, run = bench_decode(ctx, hip, K, W, args.eager)
+        value = run["bytes"] / run["seconds"] / 1e9
+        log(f"c2: {value:.1f} GB/s, {run['seconds'] * 1e6:.2f} us per step")
+        entry = {"workload": f"c2 single-token FlashDecode, L=2048, Hq=16, Hkv=8, D=128, "
+                             f"{ROTATE} rotated head-major caches, {timing}",
+                 "value": round(value, 2), "unit": "GB/s", "steps": run["steps"],
+                 "ms_per_step": round(run["seconds"] * 1e3, 6), "roofline": roofline(run, "c2")}
+        result["decode_c2"] = entry
+        checked["c2"] = (c, run, entry)
+    if "c1" in chosen:
+        c, run = bench_prefill(ctx, hip, 1, K, W, args.eager)
+        entry = {"workload": c.description + " (parity config; launch-bound)",
+                 "value": round(run["flops"] / run["seconds"] / 1e12, 3), "unit": "TFLOP/s",
+                 "steps": K, "ms_per_step": round(run["seconds"] * 1e3, 6),
+                 "roofline": roofline(run, "c1")}
+        result["prefill_c1"] = entry
+        checked["c1"] = (c, run, entry)
+    if "step" in chosen and not args.eager:
         result["decode_step"] = bench_decode_step(ctx, hip, 256)
         log(f"decode step: graph {result['decode_step']['graph_us']} us "
             f"(fused value append {result['decode_step']['graph_fused_value_us']} us, "
-            f"one launch {result['decode_step']['graph_one_launch_us']} us), "
-            f"eager {result['decode_step']['eager_us']} us")
-    if "c4" in chosen:
-        bc, bat = bench_batched_decode(ctx, hip, 20, args.eager)
-        bval = bat["bytes"] / bat["seconds"] / 1e9
-        log(f"batched decode: {bval:.1f} GB/s, kernel {bat['kernel_s'] * 1e6:.1f} us")
-        result["batched_decode"] = {
-            "workload": "c4 batched decode B=32, L~U[1024,8192] seeded, Hq=32, Hkv=8, D=128",
-            "value": round(bval, 2), "unit": "GB/s", "ms_per_step": round(bat["seconds"] * 1e3, 4),
-            "roofline": hbm_roofline(bat["bytes"], bat, "c4")}
-    prefill = []
-    for config, steps in ((3, 10), (5, 2)):
-        if f"c{config}" not in chosen:
-            continue
-        if config == 5 and not mi_attn_prefill_is_mfma(ctx):
-            log("c5 skipped: FlashPrefill is not on the MFMA kernel in this build")
-            continue
-        pc, pre = bench_prefill(ctx, hip, config, steps, args.eager)
-        tflops = pre["flops"] / pre["seconds"] / 1e12
-        kt = pre["flops"] / pre["kernel_s"] / 1e12
-        log(f"prefill c{config}: {tflops:.1f} TFLOP/s, kernel {pre['kernel_s'] * 1e3:.3f} ms")
-        prefill.append({"workload": pc.description, "value": round(tflops, 2),
-                        "unit": "TFLOP/s", "ms_per_step": round(pre["seconds"] * 1e3, 4),
-                        "kernel_family": pre["plan"],
-                        "roofline": {"bound": "mfma", "achieved": round(kt, 2),
-                                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                     "frac": round(kt / MFMA_F16_PEAK_TFLOPS, 4),
-                                     "traffic": measured_traffic(f"c{config}", pre["kernel"]),
-                                     "kernel": pre["kernel"],
-                                     "kernel_ms": round(pre["kernel_s"] * 1e3, 4),
-                                     "algorithmic_flops": pre["flops"]}})
-    if prefill:
-        result["prefill"] = prefill
+            f"one launch {result['decode_step']['graph_one_launch_us']} us)")
     if "o_proj" in chosen:
         result["o_proj"] = bench_o_proj(ctx, hip, args.eager)
         result["neighbours"] = bench_neighbours(ctx, hip, args.eager)
     if args.copy_calibration:
         result["copy_calibration"] = copy_calibration(ctx, hip)
-    if not args.no_cpu and dc is not None:
-        log("cpu baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline(dc)
+    if not args.no_cpu and checked:
+        log("cpu baseline (oracle) and accuracy ...")
+        order = ["c1", "c2", "c3", "c4", "c5"]
+        result["cpu_baseline"] = cpu_baseline({k: checked[k] for k in order if k in checked})
+    for _, run, _ in checked.values():
+        run.pop("out", None)
     print(json.dumps(result), flush=True)
     ctx.close()
     return 0
@@ -670,19 +747,12 @@ def copy_calibration(ctx, hip) -> dict:
     cache = ctx.kv_cache(1, hkv, d, positions)
     key, _ = cache.layer(0)
     source = ctx.empty((positions, hkv, d))
-    calls, seconds = timed(ctx, hip, lambda b, i: b.copy_into_cache(source, key, 0), 3, True, 1)
+    seconds = timed(ctx, hip, lambda b, i: b.copy_into_cache(source, key, 0), 3, 0, True)
     source.free()
     cache.close()
     log(f"copy calibration: {nbytes} B read + written, {seconds * 1e6:.1f} us per copy")
-    return {"kernel": "copy_kv", "bytes_read": nbytes, "bytes_written": nbytes, "calls": calls,
+    return {"kernel": "copy_kv", "bytes_read": nbytes, "bytes_written": nbytes, "calls": 3,
             "us_per_copy": round(seconds * 1e6, 2)}
-
-
-def mi_attn_prefill_is_mfma(ctx) -> bool:
-    q = mi_attn.Tensor(mi_attn.describe(0x7F0000000000, (4096, 64, 128)))
-    k = mi_attn.Tensor(mi_attn.describe(0x7F0000000000, (20480, 8, 128)))
-    cfg = mi_attn.AttentionConfig(64, 8, 128, True, 16384)
-    return mi_attn.plan(q, k, k, cfg, mi_attn.FLASH_PREFILL)["kernel"] == "attn_prefill"
 
 
 if __name__ == "__main__":

@@ -53,6 +53,15 @@ bool vector_friendly(const mi_tensor &t, uint32_t vec) {
   return reinterpret_cast<uintptr_t>(t.data) % (vec * 2) == 0;
 }
 
+// Whether tiles of `rows` key rows can be addressed by unsigned 32-bit byte
+// offsets from a tile base (the MFMA kernels' direct and register loads):
+// both position strides non-negative and a tile spanning less than 4 GiB,
+// with a 512-byte margin for the in-row offset.
+bool pos_stride_fits_u32(int64_t k_pos, int64_t v_pos, uint32_t rows) {
+  if (k_pos < 0 || v_pos < 0) return false;
+  return (uint64_t)std::max(k_pos, v_pos) * rows * 2 + 512 < (1ull << 32);
+}
+
 // Default split size: about one workgroup per CU, but at least 128 keys
 // per split (each split costs a partial write and a merge read). Measured on
 // MI355X for the 2048-key decode: 128-key splits beat 32/64/256.
@@ -238,9 +247,10 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
   if (kind == MI_ATTN_FLASH_PREFILL && kernels::prefill_supported(p.D) &&
       vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8) &&
       (out == nullptr || vector_friendly(*out, 4)) && (uint64_t)p.T * p.G < (1ull << 31) &&
-      // A key tile's 32-bit byte offsets (64 rows) stay below 2^32.
-      (uint64_t)std::max(k->stride[0], v->stride[0]) * kernels::kPrefillBlockN * 2 + 512 <
-          (1ull << 32)) {
+      // A key tile's per-lane byte offsets (64 rows from the tile base) are
+      // unsigned 32-bit: both position strides non-negative, and 64 rows
+      // span less than 4 GiB. Other views take the rows kernel (int64).
+      pos_stride_fits_u32(k->stride[0], v->stride[0], kernels::kPrefillBlockN)) {
     p.family = Family::Prefill;
     p.kernel = "attn_prefill";
     p.threads = 256;
@@ -561,7 +571,7 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   // workgroup the same share of all sequences' keys (2 per CU). Explicit
   // split sizes keep the rows kernel.
   if (block_keys == 0 && p.D == 128 && (uint64_t)B <= kernels::kStreamMaxBatch &&
-      32 * (uint64_t)std::max(k->stride[1], v->stride[1]) * 2 < (1ull << 32)) {
+      pos_stride_fits_u32(k->stride[1], v->stride[1], 32)) {
     const uint32_t chunk = kernels::stream_chunk(p.G);
     const uint64_t units = (uint64_t)B * p.Hkv * (p.G / chunk);
     const uint32_t workgroups = 2 * std::max<uint32_t>(batch->ctx->compute_units, 1);

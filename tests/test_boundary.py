@@ -273,3 +273,25 @@ def test_small_prefill_grids_split_the_keys():
     assert 2 <= p["splits"] <= 8 and p["block_keys"] % 64 == 0
     assert p["splits"] * p["block_keys"] >= 1024 > (p["splits"] - 1) * p["block_keys"]
     assert _pieces(1024, 2, 1024, 0, p["block_keys"])[0] * 8 <= 2 * 256
+
+
+def test_prefill_needs_non_negative_position_strides():
+    """The MFMA prefill kernel addresses a key tile with unsigned 32-bit byte
+    offsets from the tile base, so K or V views whose position stride is
+    negative (a reversed cache) or spans 4 GiB per tile take the rows kernel,
+    which uses 64-bit offsets."""
+    L, hkv, d = 2048, 8, 128
+    q = tensor((L, 16, d))
+    cfg = AttentionConfig(16, 8, d, True, 0)
+    fwd = tensor((L, hkv, d))
+    # the same rows, last position first: element 0 is the last row in memory
+    rev = tensor((L, hkv, d), strides=(-hkv * d, d, 1), offset=(L - 1) * hkv * d * 2)
+    assert plan(q, fwd, fwd, cfg, FLASH_PREFILL)["kernel"] == "attn_prefill"
+    for k, v in ((rev, fwd), (fwd, rev), (rev, rev)):
+        p = plan(q, k, v, cfg, FLASH_PREFILL)
+        assert p["kernel"] == "attn_rows", (k.strides, v.strides, p)
+    # 64 rows at a stride of 2^25 halves span 4 GiB
+    huge = tensor((L, hkv, d), strides=(1 << 25, d, 1))
+    assert plan(q, huge, fwd, cfg, FLASH_PREFILL)["kernel"] == "attn_rows"
+    near = tensor((L, hkv, d), strides=((1 << 25) - 1024, d, 1))
+    assert plan(q, near, fwd, cfg, FLASH_PREFILL)["kernel"] == "attn_prefill"

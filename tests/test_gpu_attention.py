@@ -103,15 +103,29 @@ def test_c3_prefill_seeded(ctx):
     _prefill_parity(ctx, c, "flash-prefill")
 
 
+def tile_rows(T: int, G: int, block_m: int, rng) -> np.ndarray:
+    """Query tokens covering every row tile of the packed (token, head in
+    group) dimension: the first and last token of each tile of `block_m`
+    packed rows plus one seeded interior token. Every query head of those
+    tokens is checked, so every (row tile, KV head) piece is."""
+    tokens = []
+    for row0 in range(0, T * G, block_m):
+        first, last = row0 // G, min(T - 1, (row0 + block_m - 1) // G)
+        tokens += [first, last]
+        if last - first >= 2:
+            tokens.append(int(rng.integers(first + 1, last)))
+    return np.unique(np.asarray(tokens))
+
+
 def test_c5_chunked_prefill_seeded(ctx):
-    """4096 new tokens on a 16384-position cache, GQA 8:1; checked on 48 rows
-    (the first, the last and a seeded sample) against the oracle."""
+    """4096 new tokens on a 16384-position cache, GQA 8:1 (256-row tiles of
+    32 tokens, 128 per KV head): the first, last and one interior token of
+    every row tile, all 64 heads, against the oracle."""
     c = workloads.case(5)
-    rng = np.random.default_rng(55)
-    rows = np.unique(np.concatenate([np.arange(16), np.arange(c.tokens - 16, c.tokens),
-                                     rng.choice(c.tokens, 16, replace=False)]))
+    rows = tile_rows(c.tokens, c.group, 256, np.random.default_rng(55))
+    assert len(rows) == 3 * 128
     err = _prefill_parity(ctx, c, "flash-prefill", rows=rows)
-    print(f"c5 sampled rows max-abs {err:.2e}")
+    print(f"c5 {len(rows)} rows x 64 heads max-abs {err:.2e}")
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -136,7 +150,8 @@ def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
     (32, 8, 8200, 0, False)])
 def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
     """Grids of at least four 256-row workgroups per CU run the 8-wave row
-    tile; checked on 48 rows (first, last, seeded sample) against the oracle."""
+    tile; the first, last and one interior token of every 256-row tile (all
+    heads) are checked against the oracle."""
     rng = np.random.default_rng(T + hq)
     L = off + T if causal else T + 40
     q = rng.standard_normal((T, hq, 128)).astype(np.float16).view(np.uint16)
@@ -147,8 +162,7 @@ def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
                     mi_attn.AttentionConfig(hq, hkv, 128, causal, off), mi_attn.FLASH_PREFILL)
     assert info["kernel"] == "attn_prefill" and info["block_threads"] == 512, info
     out = run_attention(ctx, q, k, v, kind="flash-prefill", causal=causal, **geo)
-    rows = np.unique(np.concatenate([np.arange(16), np.arange(T - 16, T),
-                                     rng.choice(T, 16, replace=False)]))
+    rows = tile_rows(T, hq // hkv, 256, rng)
     ref = oracle_attention(q, k, v, causal=causal, rows=rows, **geo)
     assert_parity(out[rows], ref, label=f"T={T} hq={hq}")
 
@@ -429,3 +443,64 @@ def test_gqa_equals_mha_with_repeated_heads(ctx):
     mha = run_attention(ctx, q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), kind="tiled",
                         hq=hq, hkv=hq, d=d, off=L - T)
     assert max_abs(gqa, f16(mha)) <= 2 * TOL
+
+
+# ------------------------------------------- negative position strides ----
+
+@pytest.mark.parametrize("kind", ["flash-prefill", "tiled", "flash-decode"])
+def test_reversed_cache_views(ctx, kind):
+    """K/V views whose position stride is negative (the last position first
+    in memory): the MFMA kernels' 32-bit tile offsets cannot address them, so
+    the plan takes the rows kernel (64-bit offsets); outputs match the
+    oracle and the forward layout."""
+    rng = np.random.default_rng(31)
+    hq, hkv, d = 16, 8, 128
+    T, off = (300, 37) if kind != "flash-decode" else (1, 700)
+    L = off + T
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+    ko, kview = upload_kv(ctx, k, "reversed")
+    assert kview.strides[0] < 0
+    info = ctx.plan(ctx.tensor(q), kview, kview, mi_attn.AttentionConfig(hq, hkv, d, True, off),
+                    KINDS[kind])
+    assert info["kernel"] == "attn_rows", info
+    out = run_attention(ctx, q, k, v, kind=kind, layout="reversed", **geo)
+    ref = oracle_attention(q, k, v, **geo)
+    assert_parity(out, ref, label=f"reversed/{kind}")
+
+
+def test_batched_decode_reversed_cache_takes_the_rows_kernel(ctx):
+    """A batched decode over caches with a negative position stride runs the
+    rows kernel (the stream-K kernel's per-lane offsets are unsigned 32-bit)
+    and matches the oracle for every sequence."""
+    B, hq, hkv, d, cap = 3, 32, 8, 128, 600
+    lengths = [600, 17, 333]
+    rng = np.random.default_rng(41)
+    q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
+    # storage [B, Hkv, cap, D] with positions reversed; view [B, cap, Hkv, D]
+    kt = ctx.tensor(np.ascontiguousarray(k[:, ::-1].transpose(0, 2, 1, 3)))
+    vt = ctx.tensor(np.ascontiguousarray(v[:, ::-1].transpose(0, 2, 1, 3)))
+    strides = (hkv * cap * d, -d, cap * d, 1)
+    kview = kt.view((B, cap, hkv, d), strides, offset=(cap - 1) * d)
+    vview = vt.view((B, cap, hkv, d), strides, offset=(cap - 1) * d)
+    lt = ctx.tensor(np.asarray(lengths, np.uint32), mi_attn.U32)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        out = batch.attention_decode_batched(ctx.tensor(q), kview, vview, lt, cfg, 0)
+        batch.finish()
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert names == ["attn_rows_batched"], names
+    got = ctx.download(out)
+    for b in range(B):
+        n = lengths[b]
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"reversed seq {b} len {n}")

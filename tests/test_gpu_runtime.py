@@ -174,3 +174,49 @@ def test_capturing_batch_rules(ctx):
     capture.abandon()  # drops the recording, releases the arena
     q, k, v, cfg = _decode_inputs(ctx)
     assert ctx.download(ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)).shape == (1, 16, 128)
+
+
+def test_two_batches_in_flight_pipelined_decode():
+    """Pipelined decode (qwen3.rs:485-553): step n + 1 is encoded and committed
+    before step n is waited on, each batch with its own scratch arena
+    (context.rs:703-729). Batch B consumes an output that batch A leased from
+    its arena; both match the oracle and the eager calls bit for bit, the two
+    arenas are distinct, the leases outlive their batches, and a later batch
+    claims the first arena again. A fresh context, so the arenas' placement
+    does not depend on earlier tests."""
+    from helpers import assert_parity, oracle_attention
+
+    ctx = mi_attn.Context(0)
+    try:
+        L, hq, hkv, d = 1024, 16, 8, 128
+        q_host, k_host, v_host = rand(1, (1, hq, d)), rand(2, (L, hkv, d)), rand(3, (L, hkv, d))
+        q, k, v = ctx.tensor(q_host), ctx.tensor(k_host), ctx.tensor(v_host)
+        cfg = mi_attn.AttentionConfig(hq, hkv, d, True, L - 1)
+        eager_a = ctx.download(ctx.attention(q, k, v, cfg, mi_attn.FLASH_DECODE))
+        eager_b = ctx.download(ctx.attention(ctx.tensor(eager_a), k, v, cfg,
+                                             mi_attn.FLASH_DECODE))
+        a = ctx.begin_batch()
+        out_a = a.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)  # leased from A's arena
+        a.commit()
+        b = ctx.begin_batch()  # A is in flight: B claims another arena
+        out_b = b.attention(out_a, k, v, cfg, mi_attn.FLASH_DECODE)
+        b.commit()
+        # Each output is the first lease of a fresh 32 MiB arena chunk.
+        assert abs(out_a.data_ptr - out_b.data_ptr) >= 32 << 20
+        a.wait()
+        b.wait()
+        got_a, got_b = ctx.download(out_a), ctx.download(out_b)
+        assert (got_a == eager_a).all() and (got_b == eager_b).all()
+        geo = dict(hq=hq, hkv=hkv, d=d, off=L - 1)
+        assert_parity(got_a, oracle_attention(q_host, k_host, v_host, **geo), label="batch A")
+        assert_parity(got_b, oracle_attention(got_a, k_host, v_host, **geo), label="batch B")
+        ptr_a = out_a.data_ptr
+        out_a.free()
+        c = ctx.begin_batch()  # both arenas idle: the first one is claimed again
+        lease = c.empty((1, hq, d))
+        assert lease.data_ptr == ptr_a
+        c.finish()
+        lease.free()
+        out_b.free()
+    finally:
+        ctx.close()
