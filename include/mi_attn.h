@@ -288,6 +288,22 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q,
                                       uint32_t block_keys,
                                       const mi_tensor *out);
 
+/* mi_attention_decode_batched without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels, results and errors as
+ * mi_attention_decode_batched, except that the split-K partials live in a
+ * fixed per-GPU buffer of 16 MiB (kept until the process ends) instead of
+ * the batch arena: a call whose partials need more fails with
+ * MI_ERR_RESOURCE, and its launches carry no kernel-profiling events. Every
+ * call on one GPU shares that buffer, so calls that overlap on one GPU (two
+ * streams, two contexts) race; calls in one stream's order are safe. */
+mi_status mi_attention_decode_batched_noalloc(mi_batch *batch, const mi_tensor *q,
+                                              const mi_tensor *k, const mi_tensor *v,
+                                              const mi_tensor *lengths,
+                                              const mi_attention_config *config,
+                                              uint32_t block_keys, const mi_tensor *out);
+
 /* FlashDecode (block, threads) for a KV length
  * (flash_decode_configuration_for_length, context.rs:258-267): the tuned
  * entry, or untuned (128, 256). Untuned, mi_attention's FlashDecode runs the

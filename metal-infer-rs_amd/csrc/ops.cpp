@@ -291,13 +291,15 @@ void fill_info(const AttnPlan &p, mi_attention_plan_info *info) {
   info->scratch_bytes = p.scratch_bytes;
 }
 
-mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
+mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp,
+                   const ScratchSource &src = ScratchSource{}) {
   Context *ctx = batch->ctx;
   void *scratch = nullptr;
   mi_status st;
   if (p.splits > 1) {
-    if ((st = scratch_alloc(batch, p.scratch_bytes, &scratch)) != MI_OK) return st;
+    if ((st = scratch_take(batch, src, p.scratch_bytes, &scratch)) != MI_OK) return st;
   }
+  const bool events = src.fixed == nullptr;
   rp.partial = static_cast<float *>(scratch);
   rp.counters = p.fused ? ctx->split_counters : nullptr;
   rp.block_keys = p.block_keys;
@@ -306,13 +308,13 @@ mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp) {
   rp.group = p.G;
   st = launch(batch, p.kernel, [&](const kernels::Launch &s) {
     return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Split, s);
-  });
+  }, events);
   if (st == MI_OK && p.splits > 1 && !p.fused)
     st = launch(batch, "attn_merge", [&](const kernels::Launch &s) {
       return kernels::launch_rows(rp, p.D, p.waves, p.chunk, kernels::RowsPhase::Merge, s);
-    });
+    }, events);
   // In-order execution makes the range reusable by later work of the batch.
-  if (scratch != nullptr) scratch_free(ctx, scratch);
+  scratch_give(ctx, src, scratch);
   return st;
 }
 
@@ -471,52 +473,11 @@ mi_status prepare_qk_norm_rope(mi_batch *batch, const mi_tensor *q, const mi_ten
   return MI_OK;
 }
 
-}  // namespace
-}  // namespace mi
-
-using namespace mi;
-
-extern "C" {
-
-mi_status mi_attention(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
-                       const mi_tensor *v, const mi_attention_config *config, int32_t kind,
-                       const mi_tensor *out) {
-  return run_attention(batch, q, k, v, config, kind, 0, 0, false, out);
-}
-
-mi_status mi_attention_flash_decode_with_block(mi_batch *batch, const mi_tensor *q,
-                                               const mi_tensor *k, const mi_tensor *v,
-                                               const mi_attention_config *config,
-                                               uint32_t block_keys, const mi_tensor *out) {
-  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, 256, true, out);
-}
-
-mi_status mi_attention_flash_decode_with_configuration(
-    mi_batch *batch, const mi_tensor *q, const mi_tensor *k, const mi_tensor *v,
-    const mi_attention_config *config, uint32_t block_keys, uint32_t threads,
-    const mi_tensor *out) {
-  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, threads, true,
-                       out);
-}
-
-mi_status mi_attention_plan(const mi_context *ctx, const mi_tensor *q, const mi_tensor *k,
-                            const mi_tensor *v, const mi_attention_config *config, int32_t kind,
-                            uint32_t block_keys, uint32_t threads,
-                            mi_attention_plan_info *info) {
-  if (info == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null plan output");
-  AttnPlan p;
-  const bool explicit_flash = block_keys != 0 || threads != 0;
-  mi_status st = plan_attention(ctx, q, k, v, config, kind, block_keys, threads,
-                                explicit_flash, nullptr, &p);
-  if (st != MI_OK) return st;
-  fill_info(p, info);
-  return MI_OK;
-}
-
-mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
-                                      const mi_tensor *v, const mi_tensor *lengths,
-                                      const mi_attention_config *config, uint32_t block_keys,
-                                      const mi_tensor *out) {
+// mi_attention_decode_batched with the split partials from `src`.
+mi_status decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                         const mi_tensor *v, const mi_tensor *lengths,
+                         const mi_attention_config *config, uint32_t block_keys,
+                         const mi_tensor *out, const ScratchSource &src) {
   if (batch == nullptr || q == nullptr || k == nullptr || v == nullptr || lengths == nullptr ||
       config == nullptr || out == nullptr)
     return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
@@ -579,14 +540,14 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
       rp.group = p.G, rp.head_chunks = p.G / chunk;
       const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
       void *scratch = nullptr;
-      if ((st = scratch_alloc(batch, bytes, &scratch)) != MI_OK) return st;
+      if ((st = scratch_take(batch, src, bytes, &scratch)) != MI_OK) return st;
       rp.partial = static_cast<float *>(scratch);
       rp.counters = batch->ctx->split_counters;
       st = launch(batch, "attn_decode_stream", [&](const kernels::Launch &s) {
         return kernels::launch_decode_stream(rp, chunk, workgroups, s);
-      });
+      }, src.fixed == nullptr);
       // In-order execution makes the range reusable by later work of the batch.
-      scratch_free(batch->ctx, scratch);
+      scratch_give(batch->ctx, src, scratch);
       return st;
     }
   }
@@ -599,7 +560,70 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const
   if ((st = plan_rows(batch->ctx, &p, (uint64_t)B, p.L, block_keys, 256, true)) != MI_OK)
     return st;
   p.kernel = "attn_rows_batched";
-  return run_rows(batch, p, rp);
+  return run_rows(batch, p, rp, src);
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" {
+
+mi_status mi_attention(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                       const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                       const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, kind, 0, 0, false, out);
+}
+
+mi_status mi_attention_flash_decode_with_block(mi_batch *batch, const mi_tensor *q,
+                                               const mi_tensor *k, const mi_tensor *v,
+                                               const mi_attention_config *config,
+                                               uint32_t block_keys, const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, 256, true, out);
+}
+
+mi_status mi_attention_flash_decode_with_configuration(
+    mi_batch *batch, const mi_tensor *q, const mi_tensor *k, const mi_tensor *v,
+    const mi_attention_config *config, uint32_t block_keys, uint32_t threads,
+    const mi_tensor *out) {
+  return run_attention(batch, q, k, v, config, MI_ATTN_FLASH_DECODE, block_keys, threads, true,
+                       out);
+}
+
+mi_status mi_attention_plan(const mi_context *ctx, const mi_tensor *q, const mi_tensor *k,
+                            const mi_tensor *v, const mi_attention_config *config, int32_t kind,
+                            uint32_t block_keys, uint32_t threads,
+                            mi_attention_plan_info *info) {
+  if (info == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null plan output");
+  AttnPlan p;
+  const bool explicit_flash = block_keys != 0 || threads != 0;
+  mi_status st = plan_attention(ctx, q, k, v, config, kind, block_keys, threads,
+                                explicit_flash, nullptr, &p);
+  if (st != MI_OK) return st;
+  fill_info(p, info);
+  return MI_OK;
+}
+
+mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
+                                      const mi_tensor *v, const mi_tensor *lengths,
+                                      const mi_attention_config *config, uint32_t block_keys,
+                                      const mi_tensor *out) {
+  return decode_batched(batch, q, k, v, lengths, config, block_keys, out, ScratchSource{});
+}
+
+mi_status mi_attention_decode_batched_noalloc(mi_batch *batch, const mi_tensor *q,
+                                              const mi_tensor *k, const mi_tensor *v,
+                                              const mi_tensor *lengths,
+                                              const mi_attention_config *config,
+                                              uint32_t block_keys, const mi_tensor *out) {
+  if (batch == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null batch, tensor or config");
+  ScratchSource src;
+  src.fixed = noalloc_scratch(batch->ctx->device);
+  src.limit = kNoAllocScratchBytes;
+  if (src.fixed == nullptr)
+    return fail(MI_ERR_RESOURCE, "the no-allocation scratch is not set up on this device");
+  return decode_batched(batch, q, k, v, lengths, config, block_keys, out, src);
 }
 
 mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx, uint64_t length,

@@ -185,6 +185,20 @@ mi_status scratch_free(Context *ctx, void *ptr) {
   return MI_OK;
 }
 
+mi_status scratch_take(Batch *batch, const ScratchSource &src, size_t bytes, void **out) {
+  if (src.fixed == nullptr) return scratch_alloc(batch, bytes, out);
+  if (bytes > src.limit)
+    return fail(MI_ERR_RESOURCE, "scratch of " + std::to_string(bytes) +
+                                     " bytes exceeds the no-allocation buffer of " +
+                                     std::to_string(src.limit) + " bytes");
+  *out = src.fixed;
+  return MI_OK;
+}
+
+void scratch_give(Context *ctx, const ScratchSource &src, void *ptr) {
+  if (src.fixed == nullptr && ptr != nullptr) scratch_free(ctx, ptr);
+}
+
 }  // namespace mi
 
 using namespace mi;
@@ -245,6 +259,13 @@ mi_status mi_context_create(int32_t device, mi_context **out) {
   }
   ctx->split_counter_count = counters;
   ctx->allocated += counters * sizeof(uint32_t);
+  // The no-allocation entry point's fixed scratch on this device.
+  mi_status st = noalloc_init(device);
+  if (st != MI_OK) {
+    hipFree(ctx->split_counters);
+    hipStreamDestroy(ctx->stream);
+    return st;
+  }
   *out = ctx.release();
   return MI_OK;
 }

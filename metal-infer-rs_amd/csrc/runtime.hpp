@@ -118,15 +118,39 @@ struct Batch {
 mi_status scratch_alloc(Batch *batch, size_t bytes, void **out);
 mi_status scratch_free(Context *ctx, void *ptr);
 
+// Where one operation's scratch (split-K partials) comes from: the batch
+// arena when `fixed` is null, else the fixed device buffer `fixed` of
+// `limit` bytes (the no-allocation entry point). Launches of an operation
+// with a fixed buffer carry no profiling events either, so it calls no
+// allocating HIP routine.
+struct ScratchSource {
+  void *fixed = nullptr;
+  size_t limit = 0;
+};
+// scratch_take: the arena lease, or the fixed buffer when `bytes` fits it
+// (MI_ERR_RESOURCE naming both sizes when it does not). scratch_give
+// returns an arena lease; nothing for the fixed buffer.
+mi_status scratch_take(Batch *batch, const ScratchSource &src, size_t bytes, void **out);
+void scratch_give(Context *ctx, const ScratchSource &src, void *ptr);
+
+// The no-allocation entry point's fixed scratch: a file-scope device array
+// of kNoAllocScratchBytes (csrc/noalloc.hip), one copy per GPU, held until
+// the process ends. noalloc_init resolves its address on `device` (which
+// must be current) once per device; noalloc_scratch returns that address,
+// or null when it was never resolved.
+constexpr size_t kNoAllocScratchBytes = 16ull << 20;
+mi_status noalloc_init(int device);
+void *noalloc_scratch(int device);
+
 
 // Launches through `fn` on the batch stream. With kernel profiling on, the
 // launch carries start / stop events bound to the kernel's dispatch (see
 // kernels::Launch). `fn` returns the launch's hipError_t.
 template <typename Fn>
-mi_status launch(Batch *batch, const char *kernel, Fn &&fn) {
+mi_status launch(Batch *batch, const char *kernel, Fn &&fn, bool events = true) {
   kernels::Launch l;
   l.stream = batch->ctx->stream;
-  if (batch->ctx->profiling && !batch->capturing) {
+  if (events && batch->ctx->profiling && !batch->capturing) {
     if (hipEventCreate(&l.start) != hipSuccess || hipEventCreate(&l.stop) != hipSuccess) {
       if (l.start) hipEventDestroy(l.start);
       return fail(MI_ERR_PROFILING, "could not create profiling events");

@@ -135,6 +135,9 @@ def _load() -> ctypes.CDLL:
                                              _P(PlanInfo)]),
         "mi_attention_decode_batched": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T,
                                                        _P(AttentionConfig), ctypes.c_uint32, T]),
+        "mi_attention_decode_batched_noalloc": (ctypes.c_int, [ctypes.c_void_p, T, T, T, T,
+                                                               _P(AttentionConfig),
+                                                               ctypes.c_uint32, T]),
         "mi_flash_decode_configuration_for_length": (
             ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, _P(ctypes.c_uint32),
                            _P(ctypes.c_uint32)]),
@@ -492,6 +495,16 @@ class Batch:
                                  out=None) -> Tensor:
         out = self._out(q.shape, out)
         _check(lib().mi_attention_decode_batched(
+            self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(v.desc),
+            ctypes.byref(lengths.desc), ctypes.byref(config), block_keys,
+            ctypes.byref(out.desc)))
+        return out
+
+    def attention_decode_batched_noalloc(self, q, k, v, lengths, config, block_keys,
+                                         out: Tensor) -> Tensor:
+        """attention_decode_batched with its split partials in the library's
+        fixed per-GPU buffer: the call allocates nothing, so `out` is required."""
+        _check(lib().mi_attention_decode_batched_noalloc(
             self.handle, ctypes.byref(q.desc), ctypes.byref(k.desc), ctypes.byref(v.desc),
             ctypes.byref(lengths.desc), ctypes.byref(config), block_keys,
             ctypes.byref(out.desc)))
