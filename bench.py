@@ -194,11 +194,13 @@ def measured_traffic(workload: str, kernel: str):
 
 
 def roofline(run: dict, workload: str) -> dict:
-    """Roofline of the step's dominant kernel. Every attention step here is
-    one kernel launch (split merges run inside it), so the kernel's average
-    launch duration over the timed region is the timed seconds per step
-    (HIP events on the launch stream); the per-dispatch event median of a
-    separate eager pass is kept as `dispatch_event_us`."""
+    """Roofline of the step's kernels: one launch per attention call (split
+    merges inside it), or for the batched decode the stream kernel and its
+    merge launch, whose summed time is the call's kernel time (BASELINE's
+    definition). The kernels' average time per call over the timed region
+    is the timed seconds per step (HIP events on the launch stream); the
+    per-dispatch event medians of a separate eager pass are kept as
+    `dispatch_event_us`."""
     secs = run["seconds"]
     if "bytes" in run:
         achieved, peak, unit, work = run["bytes"] / secs / 1e9, HBM_PEAK_GBS, "GB/s", "bytes"
@@ -240,8 +242,8 @@ def bench_batched_decode(ctx, hip, steps, warmup, eager):
     name, _, kernels = kernel_profile(ctx, enqueue, 10)
     for t in (kt, vt, q, lengths, out):
         t.free()
-    return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels, launches=1,
-                   bytes=c.algorithmic_bytes(), out=got)
+    return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels,
+                   launches=len(kernels), bytes=c.algorithmic_bytes(), out=got)
 
 
 def bench_decode(ctx, hip, steps, warmup, eager):

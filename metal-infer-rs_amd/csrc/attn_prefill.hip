@@ -454,15 +454,15 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
         p.partial + ((((size_t)tile * p.kv_heads + kvh) * WAVES + wave) * SLOTS * 64 + lane) * 2;
     {
       float *mine = wave_base + split * split_stride;
-      store_coherent2(mine, m_run, l_total);
+      store_partial2(mine, m_run, l_total);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int e = 0; e < 2; ++e)
-            store_coherent2(mine + (1 + 8 * dt + 2 * q + e) * 128, o[dt][4 * q + 2 * e],
-                            o[dt][4 * q + 2 * e + 1]);
+            store_partial2(mine + (1 + 8 * dt + 2 * q + e) * 128, o[dt][4 * q + 2 * e],
+                           o[dt][4 * q + 2 * e + 1]);
     }
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __shared__ uint32_t s_last;
@@ -470,10 +470,12 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
     const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
     if (tid == 0) {
       uint32_t *counter = p.counters + tile * p.kv_heads + kvh;
-      const uint32_t arrived =
-          __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t arrived = arrive(counter);
       const bool last = arrived == nsplit - 1;
-      if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) {
+        acquire_partials();
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       s_last = last;
     }
     __syncthreads();
@@ -489,7 +491,7 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
     for (int s = 0; s < (int)kMaxPrefillSplits; ++s) {
       if (s >= (int)nsplit) break;
       float2 ml = make_float2(m_run, l_total);
-      if (s != (int)split) ml = load_coherent2(wave_base + s * split_stride);
+      if (s != (int)split) ml = load_partial2(wave_base + s * split_stride);
       ms[s] = ml.x;
       ls[s] = ml.y;
       M = fmaxf(M, ml.x);
@@ -517,8 +519,8 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            part[dt][2 * q] = load_coherent2(src + (1 + 8 * dt + 2 * q) * 128);
-            part[dt][2 * q + 1] = load_coherent2(src + (2 + 8 * dt + 2 * q) * 128);
+            part[dt][2 * q] = load_partial2(src + (1 + 8 * dt + 2 * q) * 128);
+            part[dt][2 * q + 1] = load_partial2(src + (2 + 8 * dt + 2 * q) * 128);
           }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)

@@ -129,9 +129,7 @@ __device__ __forceinline__ void merge_range(const float *base, uint32_t nsplits,
     for (int j = 0; j < kMergeFloats / THREADS + 1; ++j) {
       const uint32_t i = tid + j * THREADS;
       if constexpr (COHERENT)  // written by other workgroups of this launch
-        staged[j] = i < total ? __hip_atomic_load(const_cast<float *>(src + i), __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : 0.0f;
+        staged[j] = i < total ? load_partial(src + i) : 0.0f;
       else
         staged[j] = i < total ? src[i] : 0.0f;
     }
@@ -509,10 +507,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     if (direct) {
       out[g * p.o_head + d] = f32_to_f16(A / L);
     } else if constexpr (FUSED) {
-      store_coherent(part + g * (D + 2) + 2 + d, A);
+      store_partial(part + g * (D + 2) + 2 + d, A);
       if (d == 0) {
-        store_coherent(part + g * (D + 2), M);
-        store_coherent(part + g * (D + 2) + 1, L);
+        store_partial(part + g * (D + 2), M);
+        store_partial(part + g * (D + 2) + 1, L);
       }
     } else {
       part[g * (D + 2) + 2 + d] = A;
@@ -530,10 +528,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     __shared__ float merge_buf[kMergeFloats];
     __syncthreads();
     if (tid == 0) {
-      const uint32_t arrived = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t arrived = arrive(p.counters + unit);
       const bool last = arrived == nsplits - 1;
-      if (last) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) {
+        acquire_partials();
+        __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       s_last = last;
     }
     __syncthreads();
@@ -552,8 +552,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
 //    segments, so each workgroup streams the same number of bytes whatever
 //    the lengths. A segment is the tail of one unit, whole units and the head
 //    of another; each such piece ends in one partial, at slot
-//    (workgroup + unit) (unique, and a unit's pieces are consecutive slots),
-//    and the last piece of a unit to finish merges them (arrival counter).
+//    (workgroup + unit) (unique, and a unit's pieces are consecutive slots).
+//    attn_stream_merge_kernel, launched next on the same stream, merges the
+//    pieces of every split unit (stream order makes the partials visible;
+//    an in-launch merge would need a release per piece, which on MI355X
+//    writes back the XCD's L2 and measured 27% slower at 32 sequences).
 //  - Per 32-key tile and wave: S^T[key][head] = K Q^T on
 //    v_mfma_f32_16x16x32_f16, K rows loaded straight into the A operand
 //    (lane (g, c) holds key c, d 8 g + 32 j) and Q^T as the B operand (head
@@ -591,16 +594,14 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
   constexpr int THREADS = WAVES * 64;
   constexpr int STAGE = KT * D;  // halves of V per wave and stage
   static_assert(WAVES * GC * D * 4 <= WAVES * STAGE * 2, "wave merge must fit a stage");
-  static_assert(kMergeFloats * 4 <= WAVES * STAGE * 2, "split merge must fit a stage");
   // Two V stages, one array each, so the compiler can tell the direct loads
-  // into one from the reads of the other. After the tile loop they hold the
-  // wave merge (a) and the split merge (b).
+  // into one from the reads of the other. After a piece's tile loop stage a
+  // holds the wave merge.
   __shared__ __attribute__((aligned(16))) uint16_t v_lds_a[WAVES * STAGE];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds_b[WAVES * STAGE];
   __shared__ float s_m[WAVES][GC];
   __shared__ float s_l[WAVES][GC];
   __shared__ uint64_t s_pre[kStreamMaxBatch + 1];  // keys of all units before sequence b
-  __shared__ uint32_t s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -847,37 +848,69 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
       if (direct) {
         out[g * p.o_head + d] = f32_to_f16(A / L);
       } else {
-        // Partials keep the max in log2-scaled units, as the rows kernel's.
-        store_coherent(part + g * (D + 2) + 2 + d, A);
+        // A piece of a split unit: its partial, for the merge launch that
+        // follows on the same stream. The max stays in log2-scaled units,
+        // as the rows kernel's.
+        part[g * (D + 2) + 2 + d] = A;
         if (d == 0) {
-          store_coherent(part + g * (D + 2), M == -INFINITY ? -INFINITY : M * c2);
-          store_coherent(part + g * (D + 2) + 1, L);
+          part[g * (D + 2)] = M == -INFINITY ? -INFINITY : M * c2;
+          part[g * (D + 2) + 1] = L;
         }
       }
-    }
-    if (!direct) {
-      // Every store of this workgroup has completed before the arrival
-      // counts; the unit's last piece merges all of them.
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      __syncthreads();
-      const uint32_t pieces = last_wg - first_wg + 1;
-      if (tid == 0) {
-        const uint32_t arrived = __hip_atomic_fetch_add(p.counters + unit, 1u, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = arrived == pieces - 1;
-        if (last) __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-      }
-      __syncthreads();
-      if (s_last != 0)
-        merge_range<D, GC, THREADS, true>(p.partial + (size_t)(first_wg + unit) * GC * (D + 2),
-                                          pieces, out, p.o_head, reinterpret_cast<float *>(v_lds_b));
     }
     // The next piece's loads overwrite both stages.
     __syncthreads();
     pos += k1 - k0;
     if (pos < end && pos >= s_pre[b + 1]) b = find_seq(pos);
   }
+}
+
+// Merges the pieces of the split units of attn_decode_stream_kernel, one
+// workgroup per unit (256 threads), in piece order: the log-sum-exp combine
+// of the reference's reduce kernels (transformer.metal:2251-2316). Recomputes
+// the stream kernel's segmentation (the key prefix sums over all sequences,
+// the segment size for p.stream_workgroups workgroups) to find the unit's
+// pieces; units held by one workgroup were written directly.
+template <int GC>
+__global__ __launch_bounds__(256) void attn_stream_merge_kernel(const RowsParams p) {
+  constexpr int D = 128, THREADS = 256;
+  __shared__ float buf[kMergeFloats];
+  __shared__ uint64_t s_part[2][THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t upb = p.kv_heads * p.head_chunks;
+  const uint32_t unit = blockIdx.x, b = unit / upb, j = unit % upb;
+  auto visible = [&](uint32_t s) -> uint32_t { return min(p.lengths[s], p.kv_length); };
+  const uint32_t len_b = visible(b);
+  if (len_b == 0) return;  // NaN, written by the stream kernel
+  // Keys of all sequences, and of those before b (each times upb units).
+  uint64_t before = 0, total = 0;
+  for (uint32_t s = tid; s < p.batch; s += THREADS) {
+    const uint64_t n = visible(s);
+    total += n;
+    if (s < b) before += n;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    before += __shfl_xor(before, d, 64);
+    total += __shfl_xor(total, d, 64);
+  }
+  if (lane == 0) s_part[0][wave] = before, s_part[1][wave] = total;
+  __syncthreads();
+  before = total = 0;
+#pragma unroll
+  for (int w = 0; w < THREADS / 64; ++w) before += s_part[0][w], total += s_part[1][w];
+  before *= upb;
+  total *= upb;
+  const uint64_t W = min((uint64_t)p.stream_workgroups, max((uint64_t)1, total / kStreamMinKeys));
+  const uint64_t seg = (total + W - 1) / W;
+  const uint64_t unit_start = before + (uint64_t)j * len_b;
+  const uint32_t first_wg = (uint32_t)(unit_start / seg);
+  const uint32_t last_wg = (uint32_t)((unit_start + len_b - 1) / seg);
+  if (first_wg == last_wg) return;
+  const uint32_t kvh = j / p.head_chunks, hc = j % p.head_chunks;
+  uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)(kvh * p.group + hc * GC) * p.o_head;
+  merge_range<D, GC, THREADS>(p.partial + (size_t)(first_wg + unit) * GC * (D + 2),
+                              last_wg - first_wg + 1, out, p.o_head, buf);
 }
 
 // Merges the split partials of one (row, KV head, head chunk) unit: the
@@ -953,8 +986,12 @@ hipError_t launch_rows_d(const RowsParams &p, uint32_t waves, uint32_t chunk,
 }
 
 template <int GC>
-hipError_t launch_stream_gc(const RowsParams &p, uint32_t workgroups, const Launch &l) {
-  return dispatch(attn_decode_stream_kernel<GC>, dim3(workgroups), dim3(kStreamWaves * 64), 0, l, p);
+hipError_t launch_stream_gc(const RowsParams &p, RowsPhase phase, const Launch &l) {
+  if (phase == RowsPhase::Split)
+    return dispatch(attn_decode_stream_kernel<GC>, dim3(p.stream_workgroups),
+                    dim3(kStreamWaves * 64), 0, l, p);
+  const uint32_t units = p.batch * p.kv_heads * p.head_chunks;
+  return dispatch(attn_stream_merge_kernel<GC>, dim3(units), dim3(256), 0, l, p);
 }
 
 }  // namespace
@@ -964,14 +1001,14 @@ uint32_t stream_chunk(uint32_t group) {
   return 1;
 }
 
-hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, uint32_t workgroups,
+hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, RowsPhase phase,
                                 const Launch &l) {
   switch (chunk) {
-    case 16: return launch_stream_gc<16>(p, workgroups, l);
-    case 8: return launch_stream_gc<8>(p, workgroups, l);
-    case 4: return launch_stream_gc<4>(p, workgroups, l);
-    case 2: return launch_stream_gc<2>(p, workgroups, l);
-    case 1: return launch_stream_gc<1>(p, workgroups, l);
+    case 16: return launch_stream_gc<16>(p, phase, l);
+    case 8: return launch_stream_gc<8>(p, phase, l);
+    case 4: return launch_stream_gc<4>(p, phase, l);
+    case 2: return launch_stream_gc<2>(p, phase, l);
+    case 1: return launch_stream_gc<1>(p, phase, l);
     default: return hipErrorInvalidValue;
   }
 }

@@ -64,6 +64,7 @@ struct RowsParams {
   uint32_t query_offset;    // ignored when lengths != null
   uint32_t block_keys;      // keys per split
   uint32_t max_splits;
+  uint32_t stream_workgroups;  // stream-K decode: workgroups of the launch
   float scale_log2;         // rsqrt(D) * log2(e)
   // Decode step (step_k != null; one token, D = 128, 8 waves): q holds the
   // raw query rows and step_k / step_v the new token's key and value rows
@@ -164,16 +165,17 @@ hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
 uint32_t rows_chunk(uint32_t group);
 
 // Batched decode (one query token per sequence, head_dim 128) on MFMA with
-// a stream-K split: `workgroups` workgroups share the keys of all sequences
-// equally (each at least kStreamMinKeys). RowsParams as for the rows kernel
-// with tokens = 1, head_chunks = group / chunk and per-sequence `lengths`
-// (required); `partial` holds
-// (workgroups + units) * chunk * (D + 2) floats and `counters` one zeroed
-// counter per unit. batch <= kStreamMaxBatch; a full 32-key tile of K or V
-// must span less than 4 GiB (32 * pos stride * 2 bytes).
+// a stream-K split: p.stream_workgroups workgroups share the keys of all
+// sequences equally (each at least kStreamMinKeys). RowsParams as for the
+// rows kernel with tokens = 1, head_chunks = group / chunk and per-sequence
+// `lengths` (required); `partial` holds (stream_workgroups + units) * chunk
+// * (D + 2) floats. The Split phase streams the keys and writes units held
+// by one workgroup directly; the Merge phase (next on the same stream)
+// merges the pieces of the others. batch <= kStreamMaxBatch; a full 32-key
+// tile of K or V must span less than 4 GiB (32 * pos stride * 2 bytes).
 constexpr uint32_t kStreamMaxBatch = 1024;
 constexpr uint32_t kStreamMinKeys = 512;
-hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, uint32_t workgroups,
+hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, RowsPhase phase,
                                 const Launch &l);
 // Head chunk of the stream kernel: the largest of 16, 8, 4, 2, 1 dividing `group`.
 uint32_t stream_chunk(uint32_t group);

@@ -529,27 +529,30 @@ mi_status decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k
   rp.kv_length = p.L, rp.causal = 1, rp.query_offset = 0;
   rp.scale_log2 = (1.0f / std::sqrt((float)p.D)) * 1.4426950408889634f;
   // Default: the stream-K MFMA kernel (head_dim 128), which gives every
-  // workgroup the same share of all sequences' keys (2 per CU). Explicit
-  // split sizes keep the rows kernel.
+  // workgroup the same share of all sequences' keys (2 per CU), then its
+  // merge launch. Explicit split sizes keep the rows kernel.
   if (block_keys == 0 && p.D == 128 && (uint64_t)B <= kernels::kStreamMaxBatch &&
       pos_stride_fits_u32(k->stride[1], v->stride[1], 32)) {
     const uint32_t chunk = kernels::stream_chunk(p.G);
     const uint64_t units = (uint64_t)B * p.Hkv * (p.G / chunk);
     const uint32_t workgroups = 2 * std::max<uint32_t>(batch->ctx->compute_units, 1);
-    if (units <= batch->ctx->split_counter_count) {
-      rp.group = p.G, rp.head_chunks = p.G / chunk;
-      const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
-      void *scratch = nullptr;
-      if ((st = scratch_take(batch, src, bytes, &scratch)) != MI_OK) return st;
-      rp.partial = static_cast<float *>(scratch);
-      rp.counters = batch->ctx->split_counters;
-      st = launch(batch, "attn_decode_stream", [&](const kernels::Launch &s) {
-        return kernels::launch_decode_stream(rp, chunk, workgroups, s);
-      }, src.fixed == nullptr);
-      // In-order execution makes the range reusable by later work of the batch.
-      scratch_give(batch->ctx, src, scratch);
-      return st;
-    }
+    rp.group = p.G, rp.head_chunks = p.G / chunk;
+    rp.stream_workgroups = workgroups;
+    const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
+    void *scratch = nullptr;
+    if ((st = scratch_take(batch, src, bytes, &scratch)) != MI_OK) return st;
+    rp.partial = static_cast<float *>(scratch);
+    const bool events = src.fixed == nullptr;
+    st = launch(batch, "attn_decode_stream", [&](const kernels::Launch &s) {
+      return kernels::launch_decode_stream(rp, chunk, kernels::RowsPhase::Split, s);
+    }, events);
+    if (st == MI_OK)
+      st = launch(batch, "attn_decode_stream_merge", [&](const kernels::Launch &s) {
+        return kernels::launch_decode_stream(rp, chunk, kernels::RowsPhase::Merge, s);
+      }, events);
+    // In-order execution makes the range reusable by later work of the batch.
+    scratch_give(batch->ctx, src, scratch);
+    return st;
   }
   // 768-key splits (measured at B=32, L ~ U[1024, 8192], whole call: 768 ->
   // 4.7 TB/s; 640-960 -> 4.5-4.7; every power of two 512-4096 -> 3.8-4.1).

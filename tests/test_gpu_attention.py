@@ -215,7 +215,8 @@ def test_c4_batched_decode_seeded(ctx):
         finally:
             ctx.set_kernel_profiling(False)
         # Default: stream-K MFMA kernel; explicit split sizes: rows kernel.
-        assert names == (["attn_decode_stream"] if block == 0 else ["attn_rows_batched"]), names
+        assert names == (["attn_decode_stream", "attn_decode_stream_merge"] if block == 0
+                         else ["attn_rows_batched"]), names
         got = ctx.download(out)
         worst = 0.0
         for b in range(B):
@@ -298,7 +299,7 @@ def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
             names = [name for name, _ in ctx.take_kernel_profiles()]
         finally:
             ctx.set_kernel_profiling(False)
-        assert names == ["attn_decode_stream"], names
+        assert names == ["attn_decode_stream", "attn_decode_stream_merge"], names
         got = ctx.download(out)
         for b in range(B):
             n = min(int(lengths[b]), cap)
@@ -332,7 +333,7 @@ def test_batched_decode_stream_k_token_major_cache(ctx):
         names = [name for name, _ in ctx.take_kernel_profiles()]
     finally:
         ctx.set_kernel_profiling(False)
-    assert names == ["attn_decode_stream"], names
+    assert names == ["attn_decode_stream", "attn_decode_stream_merge"], names
     got = ctx.download(out)
     for b in range(B):
         n = lengths[b]
