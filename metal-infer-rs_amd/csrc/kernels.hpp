@@ -151,6 +151,9 @@ struct PrefillParams {
   uint32_t *counters;
   uint32_t split_tiles;
   uint32_t splits;
+  // Non-empty pieces per KV head when split (0: unsplit); the launch has
+  // exactly pieces_per_head * kv_heads workgroups, heaviest row tiles first.
+  uint32_t pieces_per_head;
 };
 
 // Split pass (one workgroup per key block; writes the output directly when a
@@ -247,7 +250,8 @@ constexpr uint32_t kMaxPrefillSplits = 8;
 // (each lane holds D / 2 values of its row).
 constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim / 4; }
 bool prefill_supported(uint32_t head_dim);
-// Grid (row_tiles, kv_heads, splits); one launch, split merges included.
+// One launch, split merges included: grid (row_tiles, kv_heads), or the
+// pieces_per_head * kv_heads non-empty pieces when the keys are split.
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
 // Capacity of a context's split-K arrival counters (row tiles x KV heads of
 // a split prefill grid).

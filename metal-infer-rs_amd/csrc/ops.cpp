@@ -28,6 +28,7 @@ struct AttnPlan {
   uint32_t grid[3] = {0, 0, 0};
   uint32_t threads = 0;
   uint32_t block_m = kernels::kPrefillBlockM;  // prefill: packed rows per workgroup
+  uint64_t pieces = 0;           // prefill key splits: non-empty pieces per KV head
   const char *kernel = "";
 };
 
@@ -157,6 +158,7 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
     for (uint32_t n : tiles) pieces += ceil_div(n, per_split);
     if (splits < 2 || pieces * p->grid[1] > 2 * cus) continue;
     p->splits = splits;
+    p->pieces = pieces;
     p->block_keys = per_split * kernels::kPrefillBlockN;
     p->grid[2] = splits;
     p->scratch_bytes = (uint64_t)splits * wgs * 4 * kernels::kPrefillPartialSlots(p->D) * 64 *
@@ -375,6 +377,7 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     pp.scale_log2 = scale * log2e;
     pp.splits = p.splits;
     pp.split_tiles = p.splits > 1 ? p.block_keys / kernels::kPrefillBlockN : 0;
+    pp.pieces_per_head = p.splits > 1 ? (uint32_t)p.pieces : 0;
     void *scratch = nullptr;
     mi_status st;
     if (p.splits > 1) {
