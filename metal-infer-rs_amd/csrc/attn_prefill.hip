@@ -1,4 +1,4 @@
-// MFMA flash prefill for gfx950 (AttentionKind::FlashPrefill at D = 64, 128).
+// MFMA flash prefill for gfx950 (AttentionKind::FlashPrefill at D = 64, 128, 256).
 //
 // Replaces attention_flash_prefill_f16 (transformer.metal:1667-1822) with a
 // CDNA4 design:
@@ -61,15 +61,19 @@ constexpr int kReadAhead = 4;
 
 // BMT packed rows per workgroup, 32 per wave: 128 (4 waves, two workgroups
 // per CU) or, for D = 128 grids of at least four workgroups per CU, 256 (8
-// waves sharing each K/V tile, one workgroup per CU).
+// waves sharing each K/V tile, one workgroup per CU). D = 256 runs one
+// 4-wave workgroup per CU: its Q operand and O accumulators (64 + 128
+// registers per lane) leave room for one wave per SIMD, and its two LDS
+// stages take 141 KB.
 template <int D, int BMT>
-__global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kernel(
+__global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void attn_prefill_kernel(
     const PrefillParams p) {
   constexpr int BM = BMT;
   constexpr int THREADS = BMT * 2;
   constexpr int WAVES = THREADS / 64;
   constexpr int BPW = 16 / WAVES;     // 1 KB blocks per wave of each K / V tile
   static_assert(BM == 128 || (BM == 256 && D == 128), "row tile");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   constexpr int DC = D / 16;          // 16-wide d chunks of Q K^T
   constexpr int DT = D / 32;          // 32-row d tiles of O^T
   constexpr int KS = D + 8;           // K tile row stride (halves)
@@ -534,24 +538,30 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(o[dt][r], w, acc[dt][r]);
       } else {
+        // Up to four d tiles (64 registers) of loads in flight per round.
+        constexpr int DB = DT < 4 ? DT : 4;
         const float *src = wave_base + s * split_stride;
-        float2 part[DT][8];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int d0 = 0; d0 < DT; d0 += DB) {
+          float2 part[DB][8];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            part[dt][2 * q] = load_partial2(src + (1 + 8 * dt + 2 * q) * 128);
-            part[dt][2 * q + 1] = load_partial2(src + (2 + 8 * dt + 2 * q) * 128);
-          }
+          for (int i = 0; i < DB; ++i)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+            for (int q = 0; q < 4; ++q) {
+              part[i][2 * q] = load_partial2(src + (1 + 8 * (d0 + i) + 2 * q) * 128);
+              part[i][2 * q + 1] = load_partial2(src + (2 + 8 * (d0 + i) + 2 * q) * 128);
+            }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[dt][4 * q] = fmaf(part[dt][2 * q].x, w, acc[dt][4 * q]);
-            acc[dt][4 * q + 1] = fmaf(part[dt][2 * q].y, w, acc[dt][4 * q + 1]);
-            acc[dt][4 * q + 2] = fmaf(part[dt][2 * q + 1].x, w, acc[dt][4 * q + 2]);
-            acc[dt][4 * q + 3] = fmaf(part[dt][2 * q + 1].y, w, acc[dt][4 * q + 3]);
-          }
+          for (int i = 0; i < DB; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int dt = d0 + i;
+              acc[dt][4 * q] = fmaf(part[i][2 * q].x, w, acc[dt][4 * q]);
+              acc[dt][4 * q + 1] = fmaf(part[i][2 * q].y, w, acc[dt][4 * q + 1]);
+              acc[dt][4 * q + 2] = fmaf(part[i][2 * q + 1].x, w, acc[dt][4 * q + 2]);
+              acc[dt][4 * q + 3] = fmaf(part[i][2 * q + 1].y, w, acc[dt][4 * q + 3]);
+            }
+        }
       }
     }
 #pragma unroll
@@ -581,7 +591,7 @@ __global__ __launch_bounds__(BMT * 2, BMT == 128 ? 2 : 1) void attn_prefill_kern
 }  // namespace
 
 bool prefill_supported(uint32_t head_dim) {
-  return head_dim == 64 || head_dim == 128;
+  return head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
@@ -598,6 +608,9 @@ hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launc
         return dispatch(attn_prefill_kernel<128, 256>, grid, dim3(512), 0, l, p);
       if (p.block_m != 128) return hipErrorInvalidValue;
       return dispatch(attn_prefill_kernel<128, 128>, grid, dim3(256), 0, l, p);
+    case 256:
+      if (p.block_m != 128) return hipErrorInvalidValue;
+      return dispatch(attn_prefill_kernel<256, 128>, grid, dim3(256), 0, l, p);
     default: return hipErrorInvalidValue;
   }
 }

@@ -125,7 +125,7 @@ struct QkNormRopeParams {
   float theta, epsilon;
 };
 
-// MFMA flash prefill (FlashPrefill at head_dim 128 / 64).
+// MFMA flash prefill (FlashPrefill at head_dim 64 / 128 / 256).
 struct PrefillParams {
   const uint16_t *q;
   int64_t q_tok, q_head;
@@ -250,6 +250,8 @@ constexpr uint32_t kMaxPrefillSplits = 8;
 // (each lane holds D / 2 values of its row).
 constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim / 4; }
 bool prefill_supported(uint32_t head_dim);
+// 128-row prefill workgroups resident per CU: two, or one at head_dim 256.
+constexpr uint32_t prefill_workgroups_per_cu(uint32_t head_dim) { return head_dim == 256 ? 1 : 2; }
 // One launch, split merges included: grid (row_tiles, kv_heads), or the
 // pieces_per_head * kv_heads non-empty pieces when the keys are split.
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);

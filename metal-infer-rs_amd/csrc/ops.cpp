@@ -123,11 +123,11 @@ mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t ma
   return MI_OK;
 }
 
-// Key splits for prefill grids too small to fill the chip (fewer than two
-// workgroups per CU): the causally heavy row tiles are cut into ranges of
-// whole key tiles, so no workgroup walks the full key range while CUs idle.
-// The split count is the largest (up to kMaxPrefillSplits) whose non-empty
-// pieces still fit on the chip at once (two workgroups per CU): beyond that
+// Key splits for prefill grids too small to fill the chip (fewer than the
+// resident workgroups: two per CU, one at D = 256): the causally heavy row
+// tiles are cut into ranges of whole key tiles, so no workgroup walks the
+// full key range while CUs idle. The split count is the largest (up to
+// kMaxPrefillSplits) whose non-empty pieces still fit on the chip at once: beyond that
 // the pieces queue and each one's fixed cost (Q load, first K/V round trip,
 // partial write) outweighs the balance. The last split of a row tile to
 // finish merges the f32 partials. Problems with fewer than 8 key tiles are
@@ -137,9 +137,11 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
   p->block_keys = 0;
   const uint64_t row_tiles = p->grid[0];
   const uint64_t wgs = row_tiles * p->grid[1];
-  const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1);
+  // Resident 128-row workgroups per CU (D = 256: one, by registers and LDS).
+  const uint64_t per_cu = kernels::prefill_workgroups_per_cu(p->D);
+  const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1) * per_cu;
   const uint64_t counters = ctx ? ctx->split_counter_count : kernels::kSplitCounters;
-  if (wgs >= 2 * cus || wgs > counters) return;
+  if (wgs >= cus || wgs > counters) return;
   // Key tiles of each row tile (the kernel's causal window of its last row).
   std::vector<uint32_t> tiles(row_tiles);
   uint32_t max_tiles = 0;
@@ -156,7 +158,7 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
     const uint32_t splits = ceil_div(max_tiles, per_split);
     uint64_t pieces = 0;
     for (uint32_t n : tiles) pieces += ceil_div(n, per_split);
-    if (splits < 2 || pieces * p->grid[1] > 2 * cus) continue;
+    if (splits < 2 || pieces * p->grid[1] > cus) continue;
     p->splits = splits;
     p->pieces = pieces;
     p->block_keys = per_split * kernels::kPrefillBlockN;

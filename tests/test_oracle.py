@@ -68,6 +68,27 @@ def test_f32_to_f16_matches_numpy_rne():
 
 # ------------------------------------------------------ generator --------
 
+def test_xorshift_matches_marsaglias_published_xor64():
+    """qwen3.rs:1011-1034 is Marsaglia's xor64 (shifts 13, 7, 17; "Xorshift
+    RNGs", Journal of Statistical Software 8(14), 2003), whose published seed
+    88172645463325252 gives 8748534153485358512, 3040900993826735515,
+    3453997556048239312. A wrong shift triple or order fails this; the
+    draw is that state over 2^64 (u64::MAX as f64 + 1.0)."""
+    import ctypes
+
+    state = ctypes.c_uint64(oracle.lib().orc_xorshift_seed(88172645463325252))
+    for expected in (8748534153485358512, 3040900993826735515, 3453997556048239312):
+        draw = oracle.lib().orc_xorshift_next_f64(ctypes.byref(state))
+        assert state.value == expected
+        assert draw == expected / 2.0**64
+    # seed 0 is replaced by the golden-ratio word (qwen3.rs:1016-1023)
+    assert oracle.lib().orc_xorshift_seed(0) == 0x9E3779B97F4A7C15
+    # the package's native generator walks the same stream: its first
+    # uniform draw from this seed, scaled to [0, 2^32), is the top word
+    first = workloads.uniform_u32(88172645463325252, 0, 0xFFFFFFFE, 1)[0]
+    assert first == (8748534153485358512 * 0xFFFFFFFF) >> 64
+
+
 def test_xorshift_jump_composes():
     s = oracle.lib().orc_xorshift_seed(12345)
     assert oracle.xorshift_jump(s, 1000 + 2345) == oracle.xorshift_jump(
