@@ -157,11 +157,23 @@ def timed(ctx, hip, enqueue, steps: int, warmup: int, eager: bool) -> float:
     return seconds
 
 
-def kernel_profile(ctx: mi_attn.Context, enqueue, count: int) -> tuple[str, float, dict]:
+# Launch record of each workload's dominant kernel (used when the eager
+# per-dispatch pass is skipped).
+DOMINANT = {"c1": "attn_prefill", "c2": "attn_rows", "c3": "attn_prefill",
+            "c4": "attn_decode_stream", "c5": "attn_prefill"}
+DISPATCH_EVENTS = True  # --no-dispatch-events clears it
+
+
+def kernel_profile(ctx: mi_attn.Context, enqueue, count: int,
+                   workload: str = "") -> tuple[str, float, dict]:
     """The dominant kernel (largest total time) of `count` eager calls, its
     median duration per launch (s), and every kernel's median, from the
     start / stop events the library binds to each dispatch on the batch's
-    stream (hipExtLaunchKernelGGL). A diagnostic beside the timed region."""
+    stream (hipExtLaunchKernelGGL). A diagnostic beside the timed region;
+    skipped with --no-dispatch-events (so that a profiler's trace of the run
+    holds only the timed calls)."""
+    if not DISPATCH_EVENTS and workload in DOMINANT:
+        return DOMINANT[workload], float("nan"), {}
     ctx.take_kernel_profiles()
     ctx.set_kernel_profiling(True)
     try:
@@ -239,11 +251,11 @@ def bench_batched_decode(ctx, hip, steps, warmup, eager):
 
     seconds = timed(ctx, hip, enqueue, steps, warmup, eager)
     got = ctx.download(out)
-    name, _, kernels = kernel_profile(ctx, enqueue, 10)
+    name, _, kernels = kernel_profile(ctx, enqueue, 10, "c4")
     for t in (kt, vt, q, lengths, out):
         t.free()
     return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels,
-                   launches=len(kernels), bytes=c.algorithmic_bytes(), out=got)
+                   launches=len(kernels) or None, bytes=c.algorithmic_bytes(), out=got)
 
 
 def bench_decode(ctx, hip, steps, warmup, eager):
@@ -267,7 +279,7 @@ def bench_decode(ctx, hip, steps, warmup, eager):
     calls = max(ROTATE, (steps + ROTATE - 1) // ROTATE * ROTATE)
     seconds = timed(ctx, hip, enqueue, calls, warmup, eager)
     got = ctx.download(out)
-    name, _, kernels = kernel_profile(ctx, enqueue, 4 * ROTATE)
+    name, _, kernels = kernel_profile(ctx, enqueue, 4 * ROTATE, "c2")
     q.free()
     out.free()
     cache.close()
@@ -376,7 +388,7 @@ def bench_prefill(ctx, hip, config, steps, warmup, eager):
     plan = ctx.plan(q, key, value, cfg, kind)
     seconds = timed(ctx, hip, enqueue, steps, warmup, eager)
     got = ctx.download(out)
-    name, _, kernels = kernel_profile(ctx, enqueue, 10 if config != 5 else 3)
+    name, _, kernels = kernel_profile(ctx, enqueue, 10 if config != 5 else 3, f"c{config}")
     q.free()
     out.free()
     cache.close()
@@ -645,7 +657,12 @@ def main() -> int:
                     help="time eager launches instead of HIP graph replays (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB KV copy (PMC traffic calibration)")
+    ap.add_argument("--no-dispatch-events", action="store_true",
+                    help="skip the eager per-dispatch event pass beside each timed region "
+                         "(for a profiler trace of the timed calls only)")
     args = ap.parse_args()
+    global DISPATCH_EVENTS
+    DISPATCH_EVENTS = not args.no_dispatch_events
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the attention path has no multi-GPU "
               "component in this build; a multi-GPU layout is design-only here", file=sys.stderr)

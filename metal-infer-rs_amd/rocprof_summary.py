@@ -23,12 +23,14 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parent))
 
-# Library launch record -> rocprof kernel of each workload's dominant kernel.
+# Each workload's dominant launch record and the rocprof kernels of one call
+# (the batched decode is its stream kernel plus the merge launch; the other
+# calls are one kernel).
 DOMINANT = {
-    "c2": ("attn_rows", "attn_rows_kernel"),
-    "c4": ("attn_decode_stream", "attn_decode_stream_kernel"),
-    "c3": ("attn_prefill", "attn_prefill_kernel"),
-    "c5": ("attn_prefill", "attn_prefill_kernel"),
+    "c2": ("attn_rows", ("attn_rows_kernel",)),
+    "c4": ("attn_decode_stream", ("attn_decode_stream_kernel", "attn_stream_merge_kernel")),
+    "c3": ("attn_prefill", ("attn_prefill_kernel",)),
+    "c5": ("attn_prefill", ("attn_prefill_kernel",)),
 }
 COPY_KERNEL = "copy_kv_kernel"
 
@@ -61,7 +63,7 @@ def stats(args) -> None:
                         for a in "XYZ")
         ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
         trace[(short(r["Kernel_Name"]), grid)].append(ns / 1e3)
-    print(f"# Kernel durations: {args.title}\n")
+    print(f"# Kernel durations: {args.title}\n" if args.title else "# Kernel durations\n")
     print(f"Command (from the repository root on the GPU box):\n\n    {args.command}\n")
     print("## Per kernel and workgroup grid (kernel trace)\n")
     print("| kernel | workgroups | calls | average (us) | median (us) | min (us) | max (us) |")
@@ -98,26 +100,30 @@ def traffic(args) -> None:
     for spec in args.run:
         workload, dirs = spec.split("=", 1)
         fetch_dir, write_dir = dirs.split(",")
-        record, kernel = DOMINANT[workload]
+        record, kernels = DOMINANT[workload]
         fetch = counter_means(fetch_dir, "FETCH_SIZE")
         write = counter_means(write_dir, "WRITE_SIZE")
         copy_kib = args.copy_bytes / 1024
         f_scale = copy_kib / fetch[COPY_KERNEL][0]
         w_scale = copy_kib / write[COPY_KERNEL][0]
-        fetch_b = fetch[kernel][0] * f_scale * 1024
-        write_b = write[kernel][0] * w_scale * 1024
+        # One dispatch of each of the call's kernels.
+        fetch_kib = sum(fetch[k][0] for k in kernels)
+        write_kib = sum(write[k][0] for k in kernels)
+        fetch_b = fetch_kib * f_scale * 1024
+        write_b = write_kib * w_scale * 1024
         case = workloads.case(int(workload[1:]), generate=False)
         algorithmic = case.algorithmic_bytes()
         out["workloads"][workload] = {
-            "kernel": record, "rocprof_kernel": kernel,
-            "dispatches": fetch[kernel][1],
-            "fetch_kib_raw": round(fetch[kernel][0], 1), "write_kib_raw": round(write[kernel][0], 1),
+            "kernel": record, "rocprof_kernels": list(kernels),
+            "dispatches": fetch[kernels[0]][1],
+            "fetch_kib_raw": round(fetch_kib, 1), "write_kib_raw": round(write_kib, 1),
             "copy_fetch_kib_raw": round(fetch[COPY_KERNEL][0], 1),
             "copy_write_kib_raw": round(write[COPY_KERNEL][0], 1),
             "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
             "fetch_bytes": int(fetch_b), "write_bytes": int(write_b),
             "traffic_bytes": int(fetch_b + write_b), "algorithmic_bytes": algorithmic,
             "traffic_over_algorithmic": round((fetch_b + write_b) / algorithmic, 3)}
+        kernel = " + ".join(kernels)
         e = out["workloads"][workload]
         lines.append(f"| {workload} | `{kernel}` | {e['dispatches']} | {e['fetch_kib_raw']:.0f} | "
                      f"{e['write_kib_raw']:.0f} | {e['fetch_scale']:.3f} / {e['write_scale']:.3f} | "

@@ -218,7 +218,8 @@ def test_c4_batched_decode_seeded(ctx):
             names = [name for name, _ in ctx.take_kernel_profiles()]
         finally:
             ctx.set_kernel_profiling(False)
-        # Default: stream-K MFMA kernel; explicit split sizes: rows kernel.
+        # Default: stream-K MFMA kernel and its merge; explicit split sizes:
+        # rows kernel.
         assert names == (["attn_decode_stream", "attn_decode_stream_merge"] if block == 0
                          else ["attn_rows_batched"]), names
         got = ctx.download(out)
@@ -228,6 +229,16 @@ def test_c4_batched_decode_seeded(ctx):
                                    off=int(c.lengths[b]) - 1)
             worst = max(worst, assert_parity(got[b:b + 1], ref, label=f"seq {b} block {block}"))
         print(f"c4 block={block}: max-abs {worst:.2e}")
+
+
+def stream_scratch_bytes(ctx, B, hq, hkv):
+    """Scratch of a default head_dim-128 batched decode: one f32 partial
+    (max, sum, acc[128]) per workgroup (2 per CU) and unit, per head of the
+    unit's head chunk."""
+    g = hq // hkv
+    chunk = next(c for c in (16, 8, 4, 2, 1) if g % c == 0)
+    units = B * hkv * (g // chunk)
+    return (2 * ctx.compute_units + units) * chunk * 130 * 4
 
 
 def _batched_case(ctx, seed, B, hq, hkv, d, cap, lengths):
@@ -282,18 +293,25 @@ def test_batched_decode_gqa_ratios_and_ragged_lengths(ctx, hq, hkv, d):
     (1, 16, 8, 20000, [20000]),
     # Many short sequences: one workgroup's segment covers many units.
     (1024, 8, 2, 24, [(b * 7) % 25 for b in range(1024)]),
+    # GQA 16 over 512 sequences (2048 units of 16 heads).
+    (512, 64, 4, 20, [1 + (b * 5) % 20 for b in range(512)]),
+    # 8192 units (more than the context's split-K arrival counters).
+    (1024, 32, 8, 12, [1 + (b * 3) % 12 for b in range(1024)]),
 ])
 def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
     """The default batched decode at head_dim 128 runs the stream-K MFMA
-    kernel: workgroups take equal shares of all sequences' keys, pieces of a
-    unit are merged by its last piece. Checked against the oracle for every
-    sequence (a zero-length one gives NaN, as the reference's 0/0), twice in
-    a row (arrival counters back at zero)."""
+    kernel: workgroups take equal shares of all sequences' keys, and a merge
+    launch combines the pieces of every split unit. Checked against the
+    oracle for every sequence (a zero-length one gives NaN, as the
+    reference's 0/0), three times in a row (every call bit-identical), and
+    bit-identical to the no-allocation entry point (its partials in the
+    library's fixed buffer) where they fit there."""
     d = 128
     q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, B + hq + cap, B, hq, hkv, d, cap, lengths)
     qt = ctx.tensor(q)
     cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
-    for rep in range(2):
+    first = None
+    for rep in range(3):
         ctx.take_kernel_profiles()
         ctx.set_kernel_profiling(True)
         try:
@@ -305,6 +323,16 @@ def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
             ctx.set_kernel_profiling(False)
         assert names == ["attn_decode_stream", "attn_decode_stream_merge"], names
         got = ctx.download(out)
+        if first is None:
+            first = got
+        else:
+            assert (got == first).all(), f"rep {rep} differs from the first call"
+        if rep == 0 and stream_scratch_bytes(ctx, B, hq, hkv) <= 16 << 20:
+            two = ctx.empty(q.shape)
+            batch = ctx.begin_batch()
+            batch.attention_decode_batched_noalloc(qt, kview, vview, lt, cfg, 0, two)
+            batch.finish()
+            assert (ctx.download(two) == got).all(), "differs from the no-allocation call"
         for b in range(B):
             n = min(int(lengths[b]), cap)
             if B > 64 and b % 41 != 0 and n != 0:

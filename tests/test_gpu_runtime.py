@@ -167,6 +167,33 @@ def test_captured_decode_step_replays_match_eager(ctx):
     cache.close()
 
 
+def test_captured_batched_decode_replays_match_eager(ctx):
+    """A graph holding the stream-K batched decode (its key split follows
+    the lengths read on the device, and its merge launch the same split)
+    replays with new queries and lengths, eager calls of the same kernels in
+    between, and every replay equals the eager call bit for bit."""
+    B, hq, hkv, d, cap = 8, 32, 8, 128, 3000
+    k, v = ctx.tensor(rand(80, (B, cap, hkv, d))), ctx.tensor(rand(81, (B, cap, hkv, d)))
+    q_in = ctx.empty((B, hq, d))
+    lengths = ctx.tensor(np.full(B, cap, np.uint32), mi_attn.U32)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    capture = ctx.begin_capture()
+    out_graph = capture.attention_decode_batched(q_in, k, v, lengths, cfg, 0)
+    graph = capture.end_capture()
+    rng = np.random.default_rng(82)
+    for rep in range(4):
+        ctx.upload(q_in, rand(90 + rep, (B, hq, d)))
+        ctx.upload(lengths, rng.integers(1, cap + 1, B).astype(np.uint32))
+        graph.launch()
+        ctx.synchronize()
+        got = ctx.download(out_graph)
+        batch = ctx.begin_batch()
+        eager = batch.attention_decode_batched(q_in, k, v, lengths, cfg, 0)
+        batch.finish()
+        assert (got == ctx.download(eager)).all(), f"replay {rep}"
+    graph.destroy()
+
+
 def test_capturing_batch_rules(ctx):
     capture = ctx.begin_capture()
     with pytest.raises(mi_attn.MiError, match="mi_batch_end_capture"):
