@@ -695,7 +695,8 @@ def main() -> int:
             "config": {"workload": "c4 batched decode (BASELINE configs[3], the largest "
                                    "single-GPU decode config): B=32, L~U[1024,8192] seeded, "
                                    "Hq=32, Hkv=8, D=128, fp16 head-major caches, one "
-                                   f"launch per step, {timing}; prefill half: c5 in prefill[]",
+                                   "call per step (the stream-K kernel and its merge "
+                                   f"launch), {timing}; prefill half: c5 in prefill[]",
                        "batch": c.batch, "kv_lengths_sum": int(c.lengths.sum()),
                        "q_heads": c.q_heads, "kv_heads": c.kv_heads, "head_dim": c.head_dim},
             "roofline": roofline(run, "c4")})

@@ -1,8 +1,9 @@
 """Summaries of rocprofv3 output for the committed profile records.
 
-  stats DIR --command CMD
+  stats DIR --command CMD [--last N]
       Markdown table of a `rocprofv3 --kernel-trace --stats --output-format csv`
-      run: calls and average / min / max duration per kernel.
+      run: calls and average / min / max duration per kernel (and, with --last,
+      the average of each kernel's last N dispatches, in trace order).
   traffic --copy-bytes N --run WORKLOAD=FETCH_DIR,WRITE_DIR ... --command CMD
       HBM bytes per dispatch of each workload's dominant kernel from two
       `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE; KiB per
@@ -58,7 +59,9 @@ def stats(args) -> None:
     several workloads, told apart by grid), then rocprofv3's own --stats
     table."""
     trace: dict[tuple[str, str], list[float]] = defaultdict(list)
-    for r in csv.DictReader(one_file(args.dir, "kernel_trace.csv").open()):
+    rows = sorted(csv.DictReader(one_file(args.dir, "kernel_trace.csv").open()),
+                  key=lambda r: int(r["Start_Timestamp"]))
+    for r in rows:
         grid = "x".join(str(int(r[f"Grid_Size_{a}"]) // int(r[f"Workgroup_Size_{a}"]))
                         for a in "XYZ")
         ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
@@ -66,11 +69,20 @@ def stats(args) -> None:
     print(f"# Kernel durations: {args.title}\n" if args.title else "# Kernel durations\n")
     print(f"Command (from the repository root on the GPU box):\n\n    {args.command}\n")
     print("## Per kernel and workgroup grid (kernel trace)\n")
-    print("| kernel | workgroups | calls | average (us) | median (us) | min (us) | max (us) |")
-    print("|---|---|---:|---:|---:|---:|---:|")
+    last = args.last
+    if last:
+        print(f"`timed average` is over each row's last {last} dispatches, which lie in "
+              "bench.py's timed region: one replay of a graph of the workload's calls (20, or "
+              "64 for c2, which rotates 64 caches). The earlier dispatches are its eager warmup "
+              "calls and one untimed replay.\n")
+    print("| kernel | workgroups | calls | average (us) | timed average (us) | median (us) | "
+          "min (us) | max (us) |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|")
     for (name, grid), us in sorted(trace.items(), key=lambda kv: -sum(kv[1])):
-        us.sort()
-        print(f"| `{name}` | {grid} | {len(us)} | {sum(us) / len(us):.2f} | "
+        tail = us[-last:] if last and len(us) >= last else []
+        timed = f"{sum(tail) / len(tail):.2f}" if tail else "—"
+        us = sorted(us)
+        print(f"| `{name}` | {grid} | {len(us)} | {sum(us) / len(us):.2f} | {timed} | "
               f"{us[len(us) // 2]:.2f} | {us[0]:.2f} | {us[-1]:.2f} |")
     rows = list(csv.DictReader(one_file(args.dir, "kernel_stats.csv").open()))
     print("\n## rocprofv3 --stats\n")
@@ -150,6 +162,8 @@ def main() -> None:
     s = sub.add_parser("stats")
     s.add_argument("dir")
     s.add_argument("--title", default="")
+    s.add_argument("--last", type=int, default=0,
+                   help="also average each kernel's last N dispatches (the timed replay)")
     s.add_argument("--command", required=True)
     t = sub.add_parser("traffic")
     t.add_argument("--copy-bytes", type=int, required=True)
