@@ -131,14 +131,14 @@ mi_status plan_rows(const Context *ctx, AttnPlan *p, uint64_t batch, uint32_t ma
 // the pieces queue and each one's fixed cost (Q load, first K/V round trip,
 // partial write) outweighs the balance. The last split of a row tile to
 // finish merges the f32 partials. Problems with fewer than 8 key tiles are
-// not split.
-void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t query_offset) {
+// not split. `block_m` is the plan's row tile and `per_cu` its resident
+// workgroups per CU.
+void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t query_offset,
+                         uint32_t block_m, uint32_t per_cu) {
   p->splits = 1;
   p->block_keys = 0;
   const uint64_t row_tiles = p->grid[0];
   const uint64_t wgs = row_tiles * p->grid[1];
-  // Resident 128-row workgroups per CU (D = 256: one, by registers and LDS).
-  const uint64_t per_cu = kernels::prefill_workgroups_per_cu(p->D);
   const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1) * per_cu;
   const uint64_t counters = ctx ? ctx->split_counter_count : kernels::kSplitCounters;
   if (wgs >= cus || wgs > counters) return;
@@ -146,7 +146,7 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
   std::vector<uint32_t> tiles(row_tiles);
   uint32_t max_tiles = 0;
   for (uint64_t t = 0; t < row_tiles; ++t) {
-    const uint64_t last_row = std::min<uint64_t>((uint64_t)p->T * p->G, (t + 1) * kernels::kPrefillBlockM) - 1;
+    const uint64_t last_row = std::min<uint64_t>((uint64_t)p->T * p->G, (t + 1) * block_m) - 1;
     const uint64_t t_last = last_row / p->G;
     const uint64_t kmax = causal ? std::min<uint64_t>(p->L, (uint64_t)query_offset + t_last + 1) : p->L;
     tiles[t] = ceil_div(kmax, kernels::kPrefillBlockN);
@@ -163,7 +163,7 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
     p->pieces = pieces;
     p->block_keys = per_split * kernels::kPrefillBlockN;
     p->grid[2] = splits;
-    p->scratch_bytes = (uint64_t)splits * wgs * 4 * kernels::kPrefillPartialSlots(p->D) * 64 *
+    p->scratch_bytes = (uint64_t)splits * wgs * (block_m / 32) * kernels::kPrefillPartialSlots(p->D) * 64 *
                        2 * sizeof(float);
     return;
   }
@@ -261,16 +261,32 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
     p.grid[0] = ceil_div((uint64_t)p.T * p.G, kernels::kPrefillBlockM);
     p.grid[1] = p.Hkv;
     p.grid[2] = 1;
-    plan_prefill_splits(ctx, &p, config->causal != 0, config->query_offset);
-    // Grids of at least four 256-row workgroups per CU take the 8-wave row
-    // tile, whose waves share each K/V tile (measured on MI355X: c5 +3%;
-    // c3, 128 such workgroups, 30% slower, so smaller grids keep 128 rows).
+    // Resident 128-row workgroups per CU: two (D = 256: one, by registers and
+    // LDS).
+    plan_prefill_splits(ctx, &p, config->causal != 0, config->query_offset,
+                        kernels::kPrefillBlockM, kernels::prefill_workgroups_per_cu(p.D));
+    // The 8-wave row tile (256 rows, one workgroup per CU) shares each K/V
+    // tile between twice the rows. Grids of at least four such workgroups per
+    // CU take it (measured on MI355X: c5 +3%; c3 unsplit, 128 such
+    // workgroups, 30% slower). So does a D = 128 grid that takes key splits,
+    // when its split at one workgroup per CU is no coarser: c3 keeps 3 x 11
+    // tiles in 256 pieces instead of 504 and ran 6% faster (42.7-43.6 against
+    // 44.8-47.6 us, bit-identical output).
     const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1);
     const uint64_t big_tiles = ceil_div((uint64_t)p.T * p.G, kernels::kPrefillBlockM2);
     if (p.splits == 1 && p.D == 128 && big_tiles * p.Hkv >= 4 * cus) {
       p.block_m = kernels::kPrefillBlockM2;
       p.threads = 512;
       p.grid[0] = (uint32_t)big_tiles;
+    } else if (p.splits > 1 && p.D == 128) {
+      AttnPlan big = p;
+      big.block_m = kernels::kPrefillBlockM2;
+      big.threads = 512;
+      big.grid[0] = (uint32_t)big_tiles;
+      big.grid[2] = 1;
+      plan_prefill_splits(ctx, &big, config->causal != 0, config->query_offset,
+                          kernels::kPrefillBlockM2, 1);
+      if (big.splits > 1 && big.block_keys <= p.block_keys) p = big;
     }
     *plan = p;
     return MI_OK;

@@ -233,33 +233,43 @@ def test_flash_prefill_routes_to_mfma_kernel():
     q = tensor((2048, 64, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
     assert p["grid"][:2] == (128, 8) and p["block_threads"] == 256
-    # c3: 2048 x 2 = 4096 packed rows -> 32 row tiles per KV head
+    # c3: 2048 x 2 = 4096 packed rows. It takes key splits, and at one 8-wave
+    # workgroup per CU its split is no coarser than with 128-row tiles at two
+    # per CU: 16 row tiles of 256 rows per KV head.
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
-    assert plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)["grid"][:2] == (32, 8)
+    p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
+    assert p["grid"][:2] == (16, 8) and p["block_threads"] == 512, p
 
 
-def _pieces(T, G, L, off, per_split_keys):
+def _pieces(T, G, L, off, per_split_keys, block_m=128):
     """Non-empty (row tile, key split) pieces of one KV head."""
     tiles = []
-    for t in range(-(-T * G // 128)):
-        t_last = (min(T * G, (t + 1) * 128) - 1) // G
+    for t in range(-(-T * G // block_m)):
+        t_last = (min(T * G, (t + 1) * block_m) - 1) // G
         tiles.append(-(-min(L, off + t_last + 1) // 64))
     per = per_split_keys // 64
     return sum(-(-n // per) for n in tiles), max(tiles)
 
 
 def test_small_prefill_grids_split_the_keys():
-    # c3: 256 workgroups on 256 CUs. The split count is the largest whose
-    # non-empty pieces all fit at two workgroups per CU: 3 splits of 11 key tiles.
+    # c3: 256 workgroups of 128 rows on 256 CUs. The split count is the largest
+    # whose non-empty pieces all fit at two workgroups per CU: 3 splits of 11
+    # key tiles. With 256-row tiles at one workgroup per CU the largest such
+    # split is the same 3 x 11 tiles, so the plan takes the 256-row tile
+    # (16 row tiles per KV head, 32 pieces each).
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
-    assert p["grid"] == (32, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
-    # (m, l) + 128 O values per row as f32, for 128 rows per row tile
-    assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 4) * 64 * 2 * 4
+    assert p["grid"] == (16, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
+    assert p["block_threads"] == 512
+    # (m, l) + 128 O values per row as f32, for 256 rows (8 waves) per row tile
+    assert p["scratch_bytes"] == 3 * 16 * 8 * 8 * (1 + 128 // 4) * 64 * 2 * 4
     pieces, max_tiles = _pieces(2048, 2, 2048, 0, p["block_keys"])
     assert pieces * 8 <= 2 * 256
     finer = -(-max_tiles // 4) * 64  # one more split would not fit
     assert _pieces(2048, 2, 2048, 0, finer)[0] * 8 > 2 * 256
+    big_pieces, big_max = _pieces(2048, 2, 2048, 0, p["block_keys"], block_m=256)
+    assert big_pieces * 8 <= 256 and big_max == max_tiles == 32
+    assert _pieces(2048, 2, 2048, 0, finer, block_m=256)[0] * 8 > 256
     # c5 fills the chip on its own: no split, no scratch
     q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
@@ -272,7 +282,9 @@ def test_small_prefill_grids_split_the_keys():
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
     assert 2 <= p["splits"] <= 8 and p["block_keys"] % 64 == 0
     assert p["splits"] * p["block_keys"] >= 1024 > (p["splits"] - 1) * p["block_keys"]
-    assert _pieces(1024, 2, 1024, 0, p["block_keys"])[0] * 8 <= 2 * 256
+    rows = 256 if p["block_threads"] == 512 else 128
+    per_cu = 1 if rows == 256 else 2
+    assert _pieces(1024, 2, 1024, 0, p["block_keys"], block_m=rows)[0] * 8 <= per_cu * 256
 
 
 def test_prefill_needs_non_negative_position_strides():
