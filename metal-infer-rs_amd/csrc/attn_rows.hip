@@ -704,9 +704,10 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
 #pragma unroll
           for (int c = 0; c < DC; ++c)
             kr[hf * DC + c] = load16_stream(reinterpret_cast<const uint16_t *>(kt + k_off[hf] + 64 * c));
+        // V is read once too: non-temporal (c4: 111.3 -> 110.1 us, same run).
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          load_lds16(reinterpret_cast<const uint16_t *>(vt + v_off[i]), vdst + i * 512);
+          load_lds16_nt(reinterpret_cast<const uint16_t *>(vt + v_off[i]), vdst + i * 512);
       } else {
         // The piece's last, partial tile: rows past it re-read its last key
         // (always in bounds) and are masked.
@@ -722,7 +723,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
           const int r = 4 * i + (lane >> 4), pc = lane & 15;
           const int chunk = 2 * ((pc >> 1) ^ stream_swizzle(r)) + (pc & 1);
           const uint32_t key = min(base + (uint32_t)stream_slot_key(r), k1 - 1);
-          load_lds16(vb + (int64_t)key * p.v_pos + chunk * 8, vdst + i * 512);
+          load_lds16_nt(vb + (int64_t)key * p.v_pos + chunk * 8, vdst + i * 512);
         }
       }
     };

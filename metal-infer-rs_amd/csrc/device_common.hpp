@@ -102,6 +102,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 __device__ __forceinline__ void load_lds16(const uint16_t *global, uint16_t *lds) {
   __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 0);
 }
+// The same with the non-temporal hint (cache policy 2: the `nt` bit), for
+// data read once, as a decode's cache rows are.
+__device__ __forceinline__ void load_lds16_nt(const uint16_t *global, uint16_t *lds) {
+  __builtin_amdgcn_global_load_lds(global, lds, 16, 0, 2);
+}
 
 // gfx950 ds_read_b64_tr_b16: within each 16-lane group, output lane 4a + b,
 // element j receives half b of the 8 bytes addressed by lane a + 4j.
