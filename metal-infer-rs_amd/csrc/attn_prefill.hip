@@ -34,6 +34,23 @@ __device__ __forceinline__ int vt_col(int key) {
   return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
 }
 
+// Direct-load tile layout (D = 64, 128): a tile row of D halves is 2D bytes
+// in 16-byte chunks, the chunks of row r XOR-swizzled so that the K operand
+// reads (16 rows, one chunk each) and the V^T transpose reads (four rows,
+// eight bytes per lane) of 16 / 32 lanes fall on distinct banks. D = 128
+// (256-byte rows span the 64 banks): K chunk ^ (r & 15), V chunk ^ 4 (r & 3).
+// D = 64 (128-byte rows, two per bank row): rows 2m and 2m + 1 already sit
+// in opposite bank halves, so K uses chunk ^ ((r >> 1) & 7) and V
+// chunk ^ 4 ((r >> 1) & 1).
+template <int D>
+__device__ __forceinline__ int k_swizzle(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int v_swizzle(int r) {
+  return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+}
+
 __device__ __forceinline__ uint4 load16(const uint16_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
@@ -71,7 +88,9 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   constexpr int BM = BMT;
   constexpr int THREADS = BMT * 2;
   constexpr int WAVES = THREADS / 64;
-  constexpr int BPW = 16 / WAVES;     // 1 KB blocks per wave of each K / V tile
+  constexpr int BPW = BN * D * 2 / 1024 / WAVES;  // 1 KB blocks per wave of each K / V tile
+  constexpr int CPR = D / 8;          // 16-byte chunks per tile row
+  constexpr int RPB = 1024 / (2 * D); // tile rows per 1 KB block
   static_assert(BM == 128 || (BM == 256 && D == 128), "row tile");
   static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   constexpr int DC = D / 16;          // 16-wide d chunks of Q K^T
@@ -83,12 +102,11 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   constexpr int V_PER = (V_JOBS + THREADS - 1) / THREADS;
   // Two LDS stages: tile i is read from one while tile i+1 is written into
   // the other, so one barrier per tile suffices.
-  // D = 128: K and V tiles arrive by direct global->LDS loads as 256-byte
-  // rows with XOR-swizzled 16-byte chunks (K: chunk ^ (key & 15), V:
-  // chunk ^ 4 (key & 3)), which keeps the K operand reads and the V^T
-  // transpose reads free of bank conflicts. Other D: register staging, K
-  // padded, V stored transposed.
-  constexpr bool DIRECT = D == 128;
+  // D = 64, 128: K and V tiles arrive by direct global->LDS loads as rows
+  // of 16-byte chunks, XOR-swizzled (k_swizzle, v_swizzle) so that the K
+  // operand reads and the V^T transpose reads are free of bank conflicts.
+  // D = 256: register staging, K padded, V stored transposed.
+  constexpr bool DIRECT = D == 64 || D == 128;
   constexpr int K_ELEMS = DIRECT ? BN * D : BN * KS;
   constexpr int V_ELEMS = DIRECT ? BN * D : D * VS;
   // One array per stage (and the stage a compile-time choice in the loop),
@@ -255,9 +273,9 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   uint32_t k_off[BPW], v_off[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int row = (wave * BPW + i) * 4 + (lane >> 4), pc = lane & 15;
-    k_off[i] = (uint32_t)(row * p.k_pos + ((pc ^ (row & 15)) * 8)) * 2u;
-    v_off[i] = (uint32_t)(row * p.v_pos + ((pc ^ ((row & 3) << 2)) * 8)) * 2u;
+    const int row = (wave * BPW + i) * RPB + lane / CPR, pc = lane % CPR;
+    k_off[i] = (uint32_t)(row * p.k_pos + ((pc ^ k_swizzle<D>(row)) * 8)) * 2u;
+    v_off[i] = (uint32_t)(row * p.v_pos + ((pc ^ v_swizzle<D>(row)) * 8)) * 2u;
   }
   auto issue_tile = [&](uint32_t ti, int stage) {
     const uint32_t j0 = ti * BN;
@@ -279,12 +297,12 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
 #pragma unroll
     for (int i = 0; i < BPW; ++i) {
       const int blk = wave * BPW + i;
-      const int row = blk * 4 + (lane >> 4);
-      const int pc = lane & 15;
+      const int row = blk * RPB + lane / CPR;
+      const int pc = lane % CPR;
       const int rr = min(row, last);
-      load_lds16(kt + (uint32_t)(rr * p.k_pos + ((pc ^ (row & 15)) * 8)),
+      load_lds16(kt + (uint32_t)(rr * p.k_pos + ((pc ^ k_swizzle<D>(row)) * 8)),
                  k_stage(stage) + blk * 512);
-      load_lds16(vt + (uint32_t)(rr * p.v_pos + ((pc ^ ((row & 3) << 2)) * 8)),
+      load_lds16(vt + (uint32_t)(rr * p.v_pos + ((pc ^ v_swizzle<D>(row)) * 8)),
                  v_stage(stage) + blk * 512);
     }
   };
@@ -318,7 +336,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       for (int c = 0; c < DC; ++c) {
         const uint16_t *kp;
         if constexpr (DIRECT)
-          kp = k_lds + (32 * mt + n) * D + (((2 * c + h) ^ (n & 15)) * 8);
+          kp = k_lds + (32 * mt + n) * D + (((2 * c + h) ^ k_swizzle<D>(n)) * 8);
         else
           kp = k_lds + (32 * mt + n) * KS + 16 * c + 8 * h;
         const h8_t a = as_h8(*reinterpret_cast<const uint4 *>(kp));
@@ -394,7 +412,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       for (int dt = 0; dt < DT; ++dt) {
         h8_t a;
         if constexpr (DIRECT) {
-          const int sw = ((4 * dt + tr_chunk) ^ (tr_j << 2)) * 8;
+          const int sw = ((4 * dt + tr_chunk) ^ v_swizzle<D>(tr_key)) * 8;
           const uint16_t *v0 = v_lds + 16 * c * D + tr_off + sw;
           const uint2 l2 = read_tr16(v0), h2 = read_tr16(v0 + 8 * D);
           a = as_h8(make_uint4(l2.x, l2.y, h2.x, h2.y));
