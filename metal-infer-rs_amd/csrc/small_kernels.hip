@@ -146,38 +146,48 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(QkNormRopeParams p) {
   }
 }
 
-// The same operations for head_dim HD in {128, 256}, with HPW head rows of
-// one token per wave, two rows per load: lane (r, q) (r = lane / 32) holds
-// elements EPL q .. EPL q + EPL - 1 of row r of each pair of rows, as one
-// 8- or 16-byte access. Lanes q < 16 hold first halves (pairs EPL q + e),
-// lanes q >= 16 the matching second halves, so a pair's partner is lane
-// q ^ 16 (v_permlane16_swap). The angles' cosines and sines depend on token
-// and pair only and are computed once per wave (one per lane, then
-// shuffled); all rows are loaded before any is written. Per element the f32 steps are the generic kernel's; the
-// row sum adds the squares in another order.
+// The same operations for head_dim HD in {128, 256} with 16-byte aligned
+// rows, HPW head rows of one token per wave. A row is spread over 16 lanes:
+// lane l of the row's 16-lane group holds elements EPL l .. EPL l + EPL - 1
+// (EPL = HD / 16, one or two 16-byte accesses), so lanes 0-7 hold the first
+// half and lanes 8-15 the matching second half. A pair's partner is then lane
+// l ^ 8 (a DPP rotate by 8 within the group), the row sum is four DPP
+// rotate-and-add steps (each lane adds the same values in the same order, so
+// all 16 agree), and each wave step covers four rows, one per group. The
+// angles depend on (token, pair) only: the wave computes each once (pair
+// lane + 64 a) and shares them through LDS. All of a wave's rows are loaded
+// before any is written. Per element the f32 steps are the generic kernel's:
+// x c - y s as x c + y (-s) and x s + y c as y c + x s, both exact
+// rewrites. The row sum adds the squares in another order.
+// DPP rotate right by K within each 16-lane row (row_ror:K).
+template <int K>
+__device__ __forceinline__ float row_ror(float x) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(x), 0x120 + K, 0xf, 0xf, false));
+}
+
 template <int HD, int HPW>
 __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams p) {
 #pragma clang fp contract(off)
-  constexpr int EPL = HD / 32, HALF = HD / 2, WORDS = EPL / 2;
-  static_assert(HPW % 2 == 0, "two rows per load");
+  constexpr int EPL = HD / 16, HALF = HD / 2, PIECES = EPL / 8, STEPS = HPW / 4;
+  static_assert(HPW % 4 == 0, "four rows per step");
+  __shared__ float s_cos[HALF], s_sin[HALF];
   const uint32_t lane = threadIdx.x;
   const uint32_t q_chunks = (p.q_heads + HPW - 1) / HPW;
   const uint32_t k_chunks = (p.kv_heads + HPW - 1) / HPW;
   const uint32_t qk_groups = p.tokens * (q_chunks + k_chunks);
   const uint32_t group = blockIdx.x;
   if (group >= qk_groups) {
-    // Value rows, two per wave (lanes 0-31 and 32-63), one 8- or 16-byte
-    // piece per lane.
-    const uint32_t row = 2 * (group - qk_groups) + (lane >> 5);
+    // Value rows, four per wave (one per 16-lane group), one or two 16-byte
+    // pieces per lane.
+    const uint32_t row = 4 * (group - qk_groups) + (lane >> 4);
     if (row >= p.tokens * p.kv_heads) return;
     const uint32_t token = row / p.kv_heads, head = row % p.kv_heads;
-    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head + EPL * (lane & 31);
+    const uint16_t *src = p.v + (int64_t)token * p.v_tok + (int64_t)head * p.v_head + EPL * (lane & 15);
     uint16_t *dst = p.v_cache + (int64_t)(p.offset + token) * p.vc_pos + (int64_t)head * p.vc_head +
-                    EPL * (lane & 31);
-    if constexpr (WORDS == 4)
-      *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
-    else
-      *reinterpret_cast<uint2 *>(dst) = *reinterpret_cast<const uint2 *>(src);
+                    EPL * (lane & 15);
+#pragma unroll
+    for (int k = 0; k < PIECES; ++k)
+      *reinterpret_cast<uint4 *>(dst + 8 * k) = *reinterpret_cast<const uint4 *>(src + 8 * k);
     return;
   }
   const uint32_t q_groups = p.tokens * q_chunks;
@@ -188,106 +198,89 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
   const uint32_t token = chunk_row / chunks;
   const uint32_t h0 = (chunk_row % chunks) * HPW;
   const uint16_t *weight = is_query ? p.q_weight : p.k_weight;
-  const uint32_t r = lane >> 5, q = lane & 31;
-  const bool first = q < 16;
-  const uint32_t e0 = EPL * q;  // this lane's first element of a row
-
-  // Each angle once per wave (lane l: pairs l + 64 a), then gathered by the
-  // lanes whose elements use it.
-  constexpr int APL = HALF / 64;
-  float ca[APL], sa[APL];
-#pragma unroll
-  for (int a = 0; a < APL; ++a) {
-    const uint32_t pair = lane + 64 * a;
-    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)HD);
-    const float angle = (float)(token + p.offset) * frequency;
-    ca[a] = cosf(angle);
-    sa[a] = sinf(angle);
-  }
-  float c[EPL], s[EPL], w[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const uint32_t pair = EPL * (q & 15) + e;
-    const int src = (int)(pair & 63);
-    if constexpr (APL == 1) {
-      c[e] = __shfl(ca[0], src, 64);
-      s[e] = __shfl(sa[0], src, 64);
-    } else {
-      const float c0 = __shfl(ca[0], src, 64), c1 = __shfl(ca[1], src, 64);
-      const float s0 = __shfl(sa[0], src, 64), s1 = __shfl(sa[1], src, 64);
-      c[e] = pair >= 64 ? c1 : c0;
-      s[e] = pair >= 64 ? s1 : s0;
-    }
-    w[e] = f16_to_f32(weight[e0 + e]);
-  }
+  const uint32_t g = lane >> 4, l = lane & 15;
+  const bool first = l < 8;
+  const uint32_t e0 = EPL * l;             // this lane's first element of a row
+  const uint32_t pair0 = EPL * (l & 7);    // ... and its first pair
   auto row_ptr = [&](uint32_t head) -> const uint16_t * {
     return is_query ? p.q + (int64_t)token * p.q_tok + (int64_t)head * p.q_head
                     : p.k + (int64_t)token * p.k_tok + (int64_t)head * p.k_head;
   };
-  uint32_t v[HPW / 2][WORDS];
+  // Every row load is issued first.
+  uint4 v[STEPS][PIECES];
 #pragma unroll
-  for (int i = 0; i < HPW / 2; ++i) {
-    const uint32_t head = h0 + 2 * i + r;
-    if (head < heads) {
-      const uint16_t *src = row_ptr(head) + e0;
-      if constexpr (WORDS == 4) {
-        const uint4 x = *reinterpret_cast<const uint4 *>(src);
-        v[i][0] = x.x, v[i][1] = x.y, v[i][2] = x.z, v[i][3] = x.w;
-      } else {
-        const uint2 x = *reinterpret_cast<const uint2 *>(src);
-        v[i][0] = x.x, v[i][1] = x.y;
-      }
-    } else {
+  for (int i = 0; i < STEPS; ++i) {
+    const uint32_t head = h0 + 4 * i + g;
 #pragma unroll
-      for (int k = 0; k < WORDS; ++k) v[i][k] = 0;
-    }
+    for (int k = 0; k < PIECES; ++k)
+      v[i][k] = head < heads ? *reinterpret_cast<const uint4 *>(row_ptr(head) + e0 + 8 * k)
+                             : make_uint4(0, 0, 0, 0);
+  }
+  // Each angle once per wave.
+#pragma unroll
+  for (int a = 0; a < HALF / 64; ++a) {
+    const uint32_t pair = lane + 64 * a;
+    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)HD);
+    const float angle = (float)(token + p.offset) * frequency;
+    s_cos[pair] = cosf(angle);
+    s_sin[pair] = sinf(angle);
+  }
+  __syncthreads();
+  float c[EPL], sn[EPL], w[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; e += 4) {
+    const float4 cv = *reinterpret_cast<const float4 *>(s_cos + pair0 + e);
+    const float4 sv = *reinterpret_cast<const float4 *>(s_sin + pair0 + e);
+    c[e] = cv.x, c[e + 1] = cv.y, c[e + 2] = cv.z, c[e + 3] = cv.w;
+    // First halves take -sin (x c + y (-s)), second halves +sin.
+    sn[e] = first ? -sv.x : sv.x, sn[e + 1] = first ? -sv.y : sv.y;
+    sn[e + 2] = first ? -sv.z : sv.z, sn[e + 3] = first ? -sv.w : sv.w;
   }
 #pragma unroll
-  for (int i = 0; i < HPW / 2; ++i) {
-    const uint32_t head = h0 + 2 * i + r;
+  for (int k = 0; k < PIECES; ++k) {
+    const uint4 wv = *reinterpret_cast<const uint4 *>(weight + e0 + 8 * k);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) w[8 * k + t] = (t & 1) ? hi_f16(ww[t >> 1]) : lo_f16(ww[t >> 1]);
+  }
+#pragma unroll
+  for (int i = 0; i < STEPS; ++i) {
+    if (h0 + 4 * i >= heads) break;  // no row of this step exists
+    const uint32_t head = h0 + 4 * i + g;
     float x[EPL];
     float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      x[e] = (e & 1) ? hi_f16(v[i][e >> 1]) : lo_f16(v[i][e >> 1]);
-      sum += x[e] * x[e];
+    for (int k = 0; k < PIECES; ++k) {
+      const uint32_t ww[4] = {v[i][k].x, v[i][k].y, v[i][k].z, v[i][k].w};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        x[8 * k + t] = (t & 1) ? hi_f16(ww[t >> 1]) : lo_f16(ww[t >> 1]);
+        sum += x[8 * k + t] * x[8 * k + t];
+      }
     }
-    // Row sum over the 32 lanes of this row.
-    for (int mask = 16; mask > 0; mask >>= 1) sum += __shfl_xor(sum, mask, 64);
+    // Row sum over the row's 16 lanes.
+    sum += row_ror<8>(sum);
+    sum += row_ror<4>(sum);
+    sum += row_ror<2>(sum);
+    sum += row_ror<1>(sum);
     const float scale = 1.0f / sqrtf(sum / (float)HD + p.epsilon);
-    float n[EPL], m[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) n[e] = x[e] * scale * w[e];
+    float out[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(n[e]), __float_as_uint(n[e]),
-                                                        false, false);
-      // The value from the other 16-lane row is whichever output differs
-      // from this lane's own input slot.
-      m[e] = __uint_as_float((lane & 16) ? sw[0] : sw[1]);
+      const float n = x[e] * scale * w[e];
+      const float m = row_ror<8>(n);  // the partner's normalised element
+      out[e] = n * c[e] + m * sn[e];
     }
     if (head < heads) {
       uint16_t *dst =
           (is_query ? p.q_out + (int64_t)token * p.qo_tok + (int64_t)head * p.qo_head
                     : p.cache + (int64_t)(p.offset + token) * p.c_pos + (int64_t)head * p.c_head) +
           e0;
-      uint32_t o[WORDS];
 #pragma unroll
-      for (int k = 0; k < WORDS; ++k) {
-        uint16_t hv[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int e = 2 * k + t;
-          // First halves: x c - y s with y the partner's; second halves:
-          // x s + y c with x the partner's.
-          hv[t] = first ? f32_to_f16(n[e] * c[e] - m[e] * s[e]) : f32_to_f16(m[e] * s[e] + n[e] * c[e]);
-        }
-        o[k] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
-      }
-      if constexpr (WORDS == 4)
-        *reinterpret_cast<uint4 *>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
-      else
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(o[0], o[1]);
+      for (int k = 0; k < PIECES; ++k)
+        *reinterpret_cast<uint4 *>(dst + 8 * k) =
+            make_uint4(pack_f16x2(out[8 * k], out[8 * k + 1]), pack_f16x2(out[8 * k + 2], out[8 * k + 3]),
+                       pack_f16x2(out[8 * k + 4], out[8 * k + 5]), pack_f16x2(out[8 * k + 6], out[8 * k + 7]));
     }
   }
 }
@@ -321,35 +314,34 @@ namespace {
 template <int HD, int HPW>
 hipError_t launch_qk_rows(const QkNormRopeParams &p, const Launch &l) {
   const uint32_t chunks = (p.q_heads + HPW - 1) / HPW + (p.kv_heads + HPW - 1) / HPW;
-  const uint32_t groups = p.tokens * chunks + (p.v != nullptr ? (p.tokens * p.kv_heads + 1) / 2 : 0u);
+  const uint32_t groups = p.tokens * chunks + (p.v != nullptr ? (p.tokens * p.kv_heads + 3) / 4 : 0u);
   if (groups == 0) return no_dispatch(l);
   return dispatch(qk_norm_rope_rows_kernel<HD, HPW>, dim3(groups), dim3(64), 0, l, p);
 }
 }  // namespace
 
 hipError_t launch_qk_norm_rope(const QkNormRopeParams &p, const Launch &l) {
-  // Many tokens (prefill): 16 head rows per wave share the angles (8: 48.8,
-  // 16: 46.2, 32: 47.3 us on c5's chunk). Few tokens
-  // (decode): two rows per wave, for the most waves in flight. Needs 8- or
-  // 16-byte aligned rows (value rows included when the value is appended).
+  // Many tokens (prefill): 32 head rows per wave at head_dim 128, 16 at 256,
+  // share the angles (c5's chunk, Q [4096, 64, 128] + K [4096, 8, 128]: 16
+  // rows 29.9-30.2 us, 32 rows 29.0-29.1, 64 rows 29.4-29.5; at head_dim 256
+  // 16 rows measured best). Few tokens (decode): four rows per wave (one per
+  // 16-lane group), for the most waves in flight. Needs 16-byte aligned rows
+  // and weights (value rows included when the value is appended).
   const bool many = p.tokens >= 16;
-  const uint32_t vec = p.head_dim / 32;
+  constexpr uint32_t vec = 8;  // halves per 16-byte access
+  auto al = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
   const bool aligned = (p.head_dim == 128 || p.head_dim == 256) && p.q_tok % vec == 0 &&
                        p.q_head % vec == 0 && p.k_tok % vec == 0 && p.k_head % vec == 0 &&
                        p.qo_tok % vec == 0 && p.qo_head % vec == 0 && p.c_pos % vec == 0 &&
-                       p.c_head % vec == 0 &&
-                       reinterpret_cast<uintptr_t>(p.q) % (2 * vec) == 0 &&
-                       reinterpret_cast<uintptr_t>(p.k) % (2 * vec) == 0 &&
-                       reinterpret_cast<uintptr_t>(p.q_out) % (2 * vec) == 0 &&
-                       reinterpret_cast<uintptr_t>(p.cache) % (2 * vec) == 0 &&
-                       (p.v == nullptr ||
-                        (p.v_tok % vec == 0 && p.v_head % vec == 0 && p.vc_pos % vec == 0 &&
-                         p.vc_head % vec == 0 && reinterpret_cast<uintptr_t>(p.v) % (2 * vec) == 0 &&
-                         reinterpret_cast<uintptr_t>(p.v_cache) % (2 * vec) == 0));
+                       p.c_head % vec == 0 && al(p.q) && al(p.k) && al(p.q_out) && al(p.cache) &&
+                       al(p.q_weight) && al(p.k_weight) &&
+                       (p.v == nullptr || (p.v_tok % vec == 0 && p.v_head % vec == 0 &&
+                                           p.vc_pos % vec == 0 && p.vc_head % vec == 0 &&
+                                           al(p.v) && al(p.v_cache)));
   if (aligned && p.head_dim == 128)
-    return many ? launch_qk_rows<128, 16>(p, l) : launch_qk_rows<128, 2>(p, l);
+    return many ? launch_qk_rows<128, 32>(p, l) : launch_qk_rows<128, 4>(p, l);
   if (aligned && p.head_dim == 256)
-    return many ? launch_qk_rows<256, 16>(p, l) : launch_qk_rows<256, 2>(p, l);
+    return many ? launch_qk_rows<256, 16>(p, l) : launch_qk_rows<256, 4>(p, l);
   const uint32_t groups =
       p.tokens * (p.q_heads + p.kv_heads) + (p.v != nullptr ? p.tokens * p.kv_heads : 0u);
   if (groups == 0) return no_dispatch(l);

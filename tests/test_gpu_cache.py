@@ -118,10 +118,11 @@ def test_qk_norm_rope_cache_seeded(ctx, offset):
 
 
 @pytest.mark.parametrize("T,hq,hkv,d,offset", [
-    (37, 20, 3, 128, 11),   # 16 rows per wave, ragged head chunks, odd KV heads
+    (37, 20, 3, 128, 11),   # 32 rows per wave: one ragged chunk, odd KV heads
+    (17, 70, 8, 128, 3),    # 32 rows per wave: three Q chunks, the last of 6 rows
     (19, 8, 2, 256, 500),   # head_dim 256, 16 rows per wave
-    (5, 6, 1, 256, 0),      # few tokens: two rows per wave
-    (3, 5, 3, 128, 2),      # odd counts in both row pairs
+    (5, 6, 1, 256, 0),      # few tokens: four rows per wave
+    (3, 5, 3, 128, 2),      # odd counts in the four-row steps
 ])
 def test_qk_norm_rope_cache_row_layouts(ctx, T, hq, hkv, d, offset):
     theta, eps = 1_000_000.0, 1e-6
