@@ -174,6 +174,65 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
   }
 }
 
+// The same rotation for 16-byte aligned rows with head_dim a multiple of 16
+// (up to 512): one workgroup per token. Its angles depend on (token, pair)
+// only, so the workgroup computes each once (one pair per thread) into LDS.
+// Then each thread rotates 8 consecutive pairs of one head: a 16-byte load of
+// the first-half elements and one of the matching second-half elements,
+// every load of the thread issued before it computes. The f32 steps per
+// element are the ones above, so the output is bit-identical.
+constexpr uint32_t kRopeRowItems = 2;  // (head, 8-pair) items per thread and round
+__global__ __launch_bounds__(256) void rope_rows_kernel(RopeParams p) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float s_cos[256], s_sin[256];
+  const uint32_t token = blockIdx.x, tid = threadIdx.x;
+  const uint32_t half = p.head_dim / 2;
+  for (uint32_t pair = tid; pair < half; pair += 256) {
+    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
+    const float angle = (float)(token + p.offset) * frequency;
+    s_cos[pair] = cosf(angle);
+    s_sin[pair] = sinf(angle);
+  }
+  __syncthreads();
+  const uint32_t per_head = half / 8;
+  const uint32_t items = p.heads * per_head;
+  const uint16_t *xt = p.x + (int64_t)token * p.x_tok;
+  uint16_t *ot = p.out + (int64_t)token * p.o_tok;
+  for (uint32_t base = 0; base < items; base += 256 * kRopeRowItems) {
+    uint4 a[kRopeRowItems], b[kRopeRowItems];
+#pragma unroll
+    for (uint32_t k = 0; k < kRopeRowItems; ++k) {
+      const uint32_t it = base + tid + 256 * k;
+      if (it < items) {
+        const uint16_t *row = xt + (int64_t)(it / per_head) * p.x_head + 8 * (it % per_head);
+        a[k] = *reinterpret_cast<const uint4 *>(row);
+        b[k] = *reinterpret_cast<const uint4 *>(row + half);
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kRopeRowItems; ++k) {
+      const uint32_t it = base + tid + 256 * k;
+      if (it >= items) continue;
+      const uint32_t pair0 = 8 * (it % per_head);
+      const uint32_t wa[4] = {a[k].x, a[k].y, a[k].z, a[k].w};
+      const uint32_t wb[4] = {b[k].x, b[k].y, b[k].z, b[k].w};
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float2 c = *reinterpret_cast<const float2 *>(s_cos + pair0 + 2 * w);
+        const float2 sn = *reinterpret_cast<const float2 *>(s_sin + pair0 + 2 * w);
+        const float a0 = lo_f16(wa[w]), a1 = hi_f16(wa[w]);
+        const float b0 = lo_f16(wb[w]), b1 = hi_f16(wb[w]);
+        lo[w] = pack_f16x2(a0 * c.x - b0 * sn.x, a1 * c.y - b1 * sn.y);
+        hi[w] = pack_f16x2(a0 * sn.x + b0 * c.x, a1 * sn.y + b1 * c.y);
+      }
+      uint16_t *orow = ot + (int64_t)(it / per_head) * p.o_head + pair0;
+      *reinterpret_cast<uint4 *>(orow) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      *reinterpret_cast<uint4 *>(orow + half) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    }
+  }
+}
+
 // Few-row matmul (the decode o_proj, matvec_f16 family of
 // transformer.metal:274-400): one wave per weight row (= output column),
 // four per workgroup. Lanes stream the row in 16-byte pieces (64 lanes cover
@@ -255,6 +314,14 @@ hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l) {
 }
 
 hipError_t launch_rope(const RopeParams &p, const Launch &l) {
+  // 16-byte rows: one workgroup per token (c5's Q [4096, 64, 128]: 30.3-31.1
+  // us with the per-thread kernel below).
+  auto al16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  if (p.head_dim % 16 == 0 && p.head_dim <= 512 && p.x_tok % 8 == 0 && p.x_head % 8 == 0 &&
+      p.o_tok % 8 == 0 && p.o_head % 8 == 0 && al16(p.x) && al16(p.out)) {
+    if (p.tokens == 0 || p.heads == 0) return no_dispatch(l);
+    return dispatch(rope_rows_kernel, dim3(p.tokens), dim3(256), 0, l, p);
+  }
   // 4-byte accesses when every row start and both halves are 4-byte aligned.
   const bool two = p.head_dim % 4 == 0 && p.x_tok % 2 == 0 && p.x_head % 2 == 0 &&
                    p.o_tok % 2 == 0 && p.o_head % 2 == 0 &&
