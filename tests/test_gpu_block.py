@@ -226,7 +226,7 @@ def rope_tolerance(oracle_bits, x_bits, offset):
 
 @pytest.mark.parametrize("T,H,D,offset,theta", [(4, 16, 128, 0, 1e6), (3, 8, 128, 2047, 1e6),
                                                 (300, 8, 128, 5, 1e6), (2, 4, 64, 16384, 1e4),
-                                                (5, 3, 8, 1, 1e4)])
+                                                (5, 3, 8, 1, 1e4), (6, 70, 256, 7, 1e6)])
 def test_rope_parity(ctx, T, H, D, offset, theta):
     x = rand(T * H + D, (T, H, D))
     got = ctx.download(ctx.rope(ctx.tensor(x), offset, theta))
@@ -235,6 +235,23 @@ def test_rope_parity(ctx, T, H, D, offset, theta):
     assert (err <= rope_tolerance(expected, x, offset)).all()
     if offset == 0:
         assert (got[0] == x[0]).all()  # position 0 is the identity
+
+
+def test_rope_aligned_and_unaligned_rows_agree_bit_for_bit(ctx):
+    """16-byte aligned rows take the per-token kernel, others the per-thread
+    kernel; both run the same f32 steps per element, so the same rows give the
+    same bits through either."""
+    T, H, D = 9, 12, 128
+    x = rand(77, (T, H, D))
+    aligned = ctx.download(ctx.rope(ctx.tensor(x), 40, 1e6))
+    # The same rows 8 bytes past a 16-byte boundary: a view at offset 4 halves.
+    store = np.zeros(T * H * D + 8, dtype=np.uint16)
+    store[4:4 + T * H * D] = x.reshape(-1)
+    shifted = ctx.tensor(store).view((T, H, D), (H * D, D, 1), offset=4)
+    unaligned = ctx.download(ctx.rope(shifted, 40, 1e6))
+    assert (aligned == unaligned).all()
+    assert (np.abs(f16(aligned).astype(np.float64) - f16(oracle.rope(x, offset=40, theta=1e6)))
+            <= rope_tolerance(oracle.rope(x, offset=40, theta=1e6), x, 40)).all()
 
 
 def test_rope_on_a_key_view_and_errors(ctx):
