@@ -265,9 +265,10 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   float l_run = 0.0f;       // this half-wave's share of the row sum
   const float c2 = p.scale_log2;
 
-  // Direct loads of tile `ti` into LDS stage `stage`: each wave fills four
-  // 1 KB blocks, lane L writing bytes 16L..16L+15 of a block, so the lane
-  // fetches the global 16 bytes that belong at that swizzled position.
+  // Direct loads of tile `ti` into LDS stage `stage`: each wave fills BPW
+  // 1 KB blocks (RPB tile rows each), lane L writing bytes 16L..16L+15 of a
+  // block, so the lane fetches the global 16 bytes that belong at that
+  // swizzled position.
   // Full tiles: loop-invariant per-lane byte offsets from a wave-uniform
   // tile base (scalar base + 32-bit vector offset per load).
   uint32_t k_off[BPW], v_off[BPW];
