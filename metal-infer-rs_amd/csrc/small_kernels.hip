@@ -170,7 +170,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
 #pragma clang fp contract(off)
   constexpr int EPL = HD / 16, HALF = HD / 2, PIECES = EPL / 8, STEPS = HPW / 4;
   static_assert(HPW % 4 == 0, "four rows per step");
-  __shared__ float s_cos[HALF], s_sin[HALF];
+  __shared__ __attribute__((aligned(16))) float s_cos[HALF], s_sin[HALF];
   const uint32_t lane = threadIdx.x;
   const uint32_t q_chunks = (p.q_heads + HPW - 1) / HPW;
   const uint32_t k_chunks = (p.kv_heads + HPW - 1) / HPW;
