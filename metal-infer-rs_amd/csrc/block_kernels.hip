@@ -1,5 +1,7 @@
 // The attention block's neighbours in the Qwen3 layer: RMSNorm and RoPE of
 // the unfused Q/K path, and the few-row matmul of the decode o_proj.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -233,6 +235,144 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeParams p) {
   }
 }
 
+// Skinny GEMM for 8 < m <= 32 rows of x (the batched-decode o_proj,
+// qwen3.rs:751-752 over B sequences): out[m, n] = x[m, k] . w[n, k]^T with
+// f32 accumulation, bound by streaming the weight once.
+//
+// One workgroup per 16 output features (weight rows), so n / 16 workgroups
+// spread over the CUs; its four waves take a quarter of k each, and the x
+// rows are the A operand of v_mfma_f32_16x16x32_f16, the weight rows the B
+// operand. Loads are coalesced: eight lanes read 128 contiguous bytes of one
+// row, a 1 KB load covering eight rows of one 64-key step. Each wave moves
+// its loads through a private LDS tile of rows of 64 keys (16-byte chunk c
+// of row r at c ^ ((r >> 1) & 7), so both the row-wise writes and the
+// MFMA-layout reads, 16 rows x one chunk, hit all 64 banks once) into MFMA
+// layout; a wave's LDS accesses execute in order, so the tile needs no
+// barrier. Chunks of CS steps alternate between two register sets: two
+// chunks of loads are in flight while one is multiplied. The four waves'
+// sums meet in LDS and add in wave order. Rows of x at or past m re-read
+// row m - 1 and are never stored.
+//
+// Measured on MI355X (graph replays, weights rotated through 512 MB): the
+// split-k alternatives (64 features per workgroup, k split over workgroups)
+// lost their gain in the cross-workgroup merge (agent-scope release per
+// workgroup, or a second launch); rotating each workgroup's chunk order and
+// masking the loads of x rows past m were slower too.
+template <int MB>
+__global__ __launch_bounds__(256) void skinny_gemm_kernel(MatvecParams p) {
+  using namespace dev;
+  constexpr int CS = kSkinnyChunkSteps;
+  constexpr int ROWS = 16 + 16 * MB;  // weight rows, then x rows
+  constexpr int LOADS = ROWS / 8;     // 1 KB loads per 64-key step
+  typedef float sf4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) uint16_t s_tile[4][CS][ROWS][64];
+  __shared__ float s_acc[4][MB][64][4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t n0 = blockIdx.x * 16;
+  const uint32_t quarter = p.k / 4, k0 = wave * quarter;
+  // Load i of a step: tile row 8 i + lane / 8, chunk lane % 8.
+  const int lrow = lane >> 3, lchunk = lane & 7;
+  const uint16_t *src[LOADS];
+  int dst[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int row = 8 * i + lrow;
+    src[i] = row < 16 ? p.w + (int64_t)(n0 + row) * p.w_row + k0 + 8 * lchunk
+                      : p.x + (int64_t)min((uint32_t)(row - 16), p.m - 1) * p.x_row + k0 + 8 * lchunk;
+    dst[i] = row * 64 + ((lchunk ^ ((row >> 1) & 7)) * 8);
+  }
+  // MFMA operands: lane (r, kg) takes chunks kg (h = 0) and kg + 4 (h = 1)
+  // of row r, keys 8 kg .. 8 kg + 7 and 32 + 8 kg .. 32 + 8 kg + 7, for the
+  // weight and the x rows alike.
+  const int r = lane & 15, kg = lane >> 4;
+  int wread[2], xread[MB][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    wread[h] = r * 64 + (((kg + 4 * h) ^ ((r >> 1) & 7)) * 8);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int xr = 16 + 16 * mb + r;
+      xread[mb][h] = xr * 64 + (((kg + 4 * h) ^ ((xr >> 1) & 7)) * 8);
+    }
+  }
+  u4_t regs[2][CS][LOADS];
+  auto load = [&](uint32_t chunk, auto set_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(set_tag)::value;
+    const uint32_t off = chunk * CS * 64;
+#pragma unroll
+    for (int s = 0; s < CS; ++s)
+#pragma unroll
+      for (int i = 0; i < LOADS; ++i)
+        regs[S][s][i] = *reinterpret_cast<const u4_t *>(src[i] + off + 64 * s);
+  };
+  auto store = [&](auto set_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(set_tag)::value;
+#pragma unroll
+    for (int s = 0; s < CS; ++s)
+#pragma unroll
+      for (int i = 0; i < LOADS; ++i)
+        *reinterpret_cast<u4_t *>(&s_tile[wave][s][0][0] + dst[i]) = regs[S][s][i];
+  };
+  sf4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = sf4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < CS; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const h8_t b = as_h8(*reinterpret_cast<const uint4 *>(&s_tile[wave][s][0][0] + wread[h]));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              as_h8(*reinterpret_cast<const uint4 *>(&s_tile[wave][s][0][0] + xread[mb][h])), b,
+              acc[mb], 0, 0, 0);
+      }
+  };
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  // The quarter is a whole number of chunk pairs; the last pair issues no
+  // further loads. The scheduling barriers keep each chunk's loads issued
+  // ahead of the multiplies.
+  const uint32_t pairs = quarter / (2 * CS * 64);
+  load(0, Set0{});
+  load(1, Set1{});
+  for (uint32_t pi = 0; pi + 1 < pairs; ++pi) {
+    store(Set0{});
+    load(2 * pi + 2, Set0{});
+    __builtin_amdgcn_sched_barrier(0);
+    compute();
+    __builtin_amdgcn_sched_barrier(0);
+    store(Set1{});
+    load(2 * pi + 3, Set1{});
+    __builtin_amdgcn_sched_barrier(0);
+    compute();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  store(Set0{});
+  compute();
+  store(Set1{});
+  compute();
+  // Lane (j, g) of block mb holds rows 16 mb + 4 g .. + 3 of feature n0 + j.
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_acc[wave][mb][lane][e] = acc[mb][e];
+  __syncthreads();
+  if (tid < 64 * MB) {
+    const int mb = tid >> 6, ln = tid & 63;
+    const uint32_t col = n0 + (ln & 15);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = ((s_acc[0][mb][ln][e] + s_acc[1][mb][ln][e]) + s_acc[2][mb][ln][e]) +
+                      s_acc[3][mb][ln][e];
+      const uint32_t row = 16 * mb + 4 * (ln >> 4) + e;
+      if (row < p.m) p.out[(int64_t)row * p.o_row + col] = f32_to_f16(v);
+    }
+  }
+}
+
 // Few-row matmul (the decode o_proj, matvec_f16 family of
 // transformer.metal:274-400): one wave per weight row (= output column),
 // four per workgroup. Lanes stream the row in 16-byte pieces (64 lanes cover
@@ -334,6 +474,19 @@ hipError_t launch_rope(const RopeParams &p, const Launch &l) {
   const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
   if (two) return dispatch(rope_kernel<2>, dim3(blocks), dim3(256), 0, l, p);
   return dispatch(rope_kernel<1>, dim3(blocks), dim3(256), 0, l, p);
+}
+
+bool skinny_gemm_supported(const MatvecParams &p, uint32_t compute_units) {
+  auto al16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  return p.m > kMatvecRows && p.m <= kSkinnyMaxRows && p.n % 16 == 0 && p.n / 16 <= compute_units &&
+         p.k % (4 * 2 * kSkinnyChunkSteps * 64) == 0 && p.x_row % 8 == 0 && p.w_row % 8 == 0 &&
+         al16(p.x) && al16(p.w);
+}
+
+hipError_t launch_skinny_gemm(const MatvecParams &p, uint32_t compute_units, const Launch &l) {
+  if (!skinny_gemm_supported(p, compute_units)) return hipErrorInvalidValue;
+  if (p.m <= 16) return dispatch(skinny_gemm_kernel<1>, dim3(p.n / 16), dim3(256), 0, l, p);
+  return dispatch(skinny_gemm_kernel<2>, dim3(p.n / 16), dim3(256), 0, l, p);
 }
 
 hipError_t launch_matvec(const MatvecParams &p, const Launch &l) {

@@ -256,14 +256,21 @@ mi_status mi_matmul(mi_batch *batch, const mi_tensor *input, const mi_tensor *we
   const int64_t ldo = m > 1 ? out->stride[0] : n;
   if (ldx < k || ldw < k || ldo < n)
     return fail(MI_ERR_SHAPE, "matmul rows overlap (row stride below the row length)");
+  p.x = static_cast<const uint16_t *>(input->data), p.x_row = ldx;
+  p.w = static_cast<const uint16_t *>(weight->data), p.w_row = ldw;
+  p.out = static_cast<uint16_t *>(out->data), p.o_row = ldo;
+  // 9 to 32 rows (the batched-decode o_proj): the skinny GEMM where the
+  // grid fits the device; it measured 9.9 us against hipBLASLt's 12.1 us for
+  // [32, 4096] x [4096, 4096]^T.
+  const uint32_t cus = batch->ctx->compute_units;
+  if (kernels::skinny_gemm_supported(p, cus))
+    return launch(batch, "skinny_gemm",
+                  [&](const kernels::Launch &l) { return kernels::launch_skinny_gemm(p, cus, l); });
   if (p.m > kernels::kMatvecRows) {
     GemmPlan *plan = nullptr;
     if ((st = gemm_plan(batch->ctx, p.m, p.n, p.k, ldx, ldw, ldo, &plan)) != MI_OK) return st;
     if (plan->ok) return run_gemm(batch, *plan, *input, *weight, *out);
   }
-  p.x = static_cast<const uint16_t *>(input->data), p.x_row = ldx;
-  p.w = static_cast<const uint16_t *>(weight->data), p.w_row = ldw;
-  p.out = static_cast<uint16_t *>(out->data), p.o_row = ldo;
   return launch(batch, "matvec",
                 [&](const kernels::Launch &l) { return kernels::launch_matvec(p, l); });
 }

@@ -33,9 +33,10 @@ hipError_t dispatch(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t l
 // A launcher with nothing to run still stamps its events, so a profiled
 // launch record always has both.
 inline hipError_t no_dispatch(const Launch &l) {
-  if (l.start != nullptr) hipEventRecord(l.start, l.stream);
-  if (l.stop != nullptr) hipEventRecord(l.stop, l.stream);
-  return hipGetLastError();
+  hipError_t err = hipSuccess;
+  if (l.start != nullptr) err = hipEventRecord(l.start, l.stream);
+  if (err == hipSuccess && l.stop != nullptr) err = hipEventRecord(l.stop, l.stream);
+  return err != hipSuccess ? err : hipGetLastError();
 }
 
 // Split-K "rows" attention: one workgroup per (sequence*token, KV head,
@@ -234,6 +235,14 @@ struct MatvecParams {
   uint32_t m, n, k;
 };
 constexpr uint32_t kMatvecRows = 8;
+// Skinny GEMM for kMatvecRows < m <= kSkinnyMaxRows, bound by streaming the
+// weight: one workgroup per 16 output features. Requires n % 16 == 0 with
+// n / 16 at most the device's CUs, k % (8 * kSkinnyChunkSteps * 64) == 0 and
+// x, w rows 16-byte aligned.
+constexpr uint32_t kSkinnyMaxRows = 32;
+constexpr uint32_t kSkinnyChunkSteps = 2;  // 64-key steps per LDS chunk
+bool skinny_gemm_supported(const MatvecParams &p, uint32_t compute_units);
+hipError_t launch_skinny_gemm(const MatvecParams &p, uint32_t compute_units, const Launch &l);
 
 hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l);
 hipError_t launch_rope(const RopeParams &p, const Launch &l);

@@ -119,6 +119,100 @@ def test_matmul_o_proj_rows(ctx, m):
     assert np.abs(f16(got) - ref).max() <= 4 * half_spacing(ref).max() + 1e-3
 
 
+def matmul_kernels(ctx, x_bits, w_bits):
+    """Launch records of one matmul call, and its output."""
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        got = run_matmul(ctx, x_bits, w_bits)
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    return names, got
+
+
+@pytest.mark.parametrize("m,n,k", [(9, 1024, 2048), (13, 1024, 2048), (17, 1024, 2048),
+                                   (24, 1024, 2048), (31, 1024, 2048), (32, 1024, 2048),
+                                   (32, 4096, 4096), (16, 16, 1024), (25, 48, 3072),
+                                   (20, 5120, 8192)])
+def test_matmul_skinny_rows(ctx, m, n, k):
+    """9 to 32 rows (the batched-decode o_proj) take the skinny GEMM when its
+    n / 16 workgroups fit the device's CUs, else the library GEMM; either way
+    the result is within the f32-summation bound of the exact product, and a
+    repeated call is bit-identical."""
+    x = rand(300 + m, (m, k))
+    w = rand(400 + n, (n, k), scale=k ** -0.5)
+    names, got = matmul_kernels(ctx, x, w)
+    assert names == (["skinny_gemm"] if n // 16 <= ctx.compute_units else ["gemm"]), names
+    check_matmul(got, x, w, f"{m}x{n}x{k}")
+    assert (run_matmul(ctx, x, w) == got).all()
+    if n * k <= 1024 * 2048:
+        ref = oracle.matmul(x, w)[1]
+        assert np.abs(f16(got) - ref).max() <= 4 * half_spacing(ref).max() + 1e-3
+
+
+def test_matmul_skinny_special_values(ctx):
+    """Zeros, a row of ones against a row of ones (the sum k exactly), and
+    products overflowing f16 to infinity, in rows spread over both 16-row
+    blocks of the skinny GEMM."""
+    m, n, k = 20, 32, 1024
+    x = np.zeros((m, k), dtype=np.float32)
+    w = np.zeros((n, k), dtype=np.float32)
+    x[3], w[5] = 1.0, 1.0
+    x[17, :4], w[30, :4] = 200.0, 200.0
+    got = f16(run_matmul(ctx, bits(x), bits(w)))
+    expected = np.zeros((m, n), dtype=np.float32)
+    expected[3, 5] = k
+    expected[3, 30] = expected[17, 5] = 800.0
+    expected[17, 30] = np.inf
+    assert np.array_equal(got, expected)
+
+
+@pytest.mark.parametrize("pad,offset", [(64, 64), (8, 8), (64, 4)])
+def test_matmul_skinny_views(ctx, pad, offset):
+    """Row strides with padding keep the skinny path when rows stay 16-byte
+    aligned; a view 8 bytes off alignment (offset 4) takes the library GEMM.
+    Both match the exact product."""
+    kernel = "gemm" if offset % 8 else "skinny_gemm"
+    m, n, k = 24, 256, 1024
+    x_store = rand(60 + pad + offset, (m, k + pad))
+    w = rand(61, (n, k), scale=k ** -0.5)
+    x_dev, w_dev = ctx.tensor(x_store), ctx.tensor(w)  # the view does not own its storage
+    x_view = x_dev.view((m, k), (k + pad, 1), offset=offset)
+    out = ctx.empty((m, n))
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        batch.matmul(x_view, w_dev, out=out)
+        batch.finish()
+        assert [name for name, _ in ctx.take_kernel_profiles()] == [kernel]
+    finally:
+        ctx.set_kernel_profiling(False)
+    flat = x_store.reshape(-1)
+    rows = np.stack([flat[offset + i * (k + pad):offset + i * (k + pad) + k] for i in range(m)])
+    check_matmul(ctx.download(out), rows, w, f"view pad={pad} offset={offset}")
+
+
+def test_captured_skinny_replays_match_eager(ctx):
+    """The skinny GEMM recorded into a graph: every replay matches the eager
+    call bit for bit."""
+    m, n, k = 32, 4096, 4096
+    x = ctx.tensor(rand(130, (m, k)))
+    w = ctx.tensor(rand(131, (n, k), scale=k ** -0.5))
+    out = ctx.empty((m, n))
+    capture = ctx.begin_capture()
+    capture.matmul(x, w, out=out)
+    graph = capture.end_capture()
+    for rep in range(3):
+        ctx.upload(x, rand(140 + rep, (m, k)))
+        graph.launch()
+        ctx.synchronize()
+        got = ctx.download(out)
+        assert (got == ctx.download(ctx.matmul(x, w))).all(), f"replay {rep}"
+    graph.destroy()
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 33, 1001), (3, 70, 7), (12, 5, 130), (1, 4096, 4096),
                                    (2, 5120, 8192)])
 def test_matmul_odd_and_large_shapes(ctx, m, n, k):
