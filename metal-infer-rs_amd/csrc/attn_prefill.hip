@@ -63,14 +63,6 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-
-
-// O and l are rescaled only when a row's max grows past its reference by
-// more than 2^8. The reference may then lag the true max, which keeps
-// P = 2^(s - m_ref) <= 256 (well inside f16) and changes nothing in O / l,
-// since both use the same reference.
-constexpr float kRescaleLog2 = 8.0f;
-
 // sched_group_barrier instruction classes (LLVM AMDGPU): MFMA, LDS read.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
@@ -356,25 +348,51 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     __builtin_amdgcn_s_setprio(0);
     // Online softmax of row n over this lane's 32 keys (MASK: causal and
     // length mask, needed only past the first row's window).
-    int lim_rel = BN;
-    if constexpr (MASK)
-      lim_rel = (int)max(min((int64_t)lim - (int64_t)j0, (int64_t)BN), (int64_t)-1);
-    float mx = -INFINITY;
+    if constexpr (MASK) {
+      const int lim_rel = (int)max(min((int64_t)lim - (int64_t)j0, (int64_t)BN), (int64_t)-1);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if constexpr (MASK) {
+        for (int r = 0; r < 16; ++r) {
           const int key_rel = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
           s[mt][r] = key_rel > lim_rel ? -INFINITY : s[mt][r];
         }
-        mx = fmaxf(mx, s[mt][r]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // m_run is the reference max; it only moves when some row of the wave
-    // outgrows it by 2^kRescaleLog2 (always on the first tile, as key 0 is
-    // visible to every row).
-    if (__any((mx - m_run) * c2 > kRescaleLog2)) {
+    }
+    // P = 2^(s c2 - m_ref c2) against the row's reference max m_run, as f16
+    // pairs in accumulator order; the row sum uses the same f16-rounded
+    // weights as P V (two partial sums, to halve the dependent chain).
+    uint32_t pw[2][8];
+    float psum;
+    auto weights = [&](float mc) __attribute__((always_inline)) {
+      float ps0 = 0.0f, ps1 = 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = exp2_raw(fmaf(s[mt][r], c2, -mc));
+          const float p1 = exp2_raw(fmaf(s[mt][r + 1], c2, -mc));
+          const uint32_t w = pack_f16x2(p0, p1);
+          pw[mt][r >> 1] = w;
+          if (r & 2)
+            ps1 = dot2(w, 0x3c003c00u, ps1);
+          else
+            ps0 = dot2(w, 0x3c003c00u, ps0);
+        }
+      psum = ps0 + ps1;
+    };
+    // The reference max moves only when a weight leaves f16's range: the
+    // row sum is then +inf (a weight rounded to f16 infinity) or NaN. A row
+    // without a reference yet (m_run = -inf, so -mc = +inf) always lands
+    // there. Until then every weight is at most 65504 = 2^16 (1 - 2^-11)
+    // times the row's largest, O and l scaling alike, with no max pass.
+    weights(m_run * c2);
+    if (__any(!(psum <= __FLT_MAX__))) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mt][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float m_new = fmaxf(m_run, mx);
       // A row that has seen no visible key yet (only possible in a later
       // key split) keeps m = -inf and nothing to rescale.
@@ -385,21 +403,8 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
       m_run = m_new;
+      weights(m_run == -INFINITY ? 0.0f : m_run * c2);
     }
-    const float mc = m_run == -INFINITY ? 0.0f : m_run * c2;
-    uint32_t pw[2][8];  // P as packed f16 pairs, in accumulator order
-    float psum = 0.0f;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = exp2_raw(fmaf(s[mt][r], c2, -mc));
-        const float p1 = exp2_raw(fmaf(s[mt][r + 1], c2, -mc));
-        const uint32_t w = pack_f16x2(p0, p1);
-        pw[mt][r >> 1] = w;
-        // The row sum uses the same f16-rounded weights as P V.
-        psum = dot2(w, 0x3c003c00u, psum);
-      }
     l_run += psum;
 
     // O^T[d][row] += V^T[d][keys] P^T[keys][row], four 16-key chunks.
