@@ -458,15 +458,28 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   const uint32_t n_full = (uint32_t)min((uint64_t)t_end, (full_lim + 1) / BN);
   // Tile t_begin + k lives in stage k & 1.
   if constexpr (DIRECT) {
+    // The first tile is computed once it (and the Q rows, loaded earlier)
+    // has landed; the second stays in flight. Loads complete in issue order,
+    // so vmcnt(2 BPW) leaves only the second tile's 2 BPW loads pending.
+    // The barrier is a bare s_barrier (no fence: a workgroup-scope fence
+    // would wait for every load, the second tile's too); each wave has
+    // waited for its own part of the first tile, and the memory clobber
+    // keeps the compiler from moving LDS reads above it.
     issue_tile(t_begin, 0);
-    if (t_begin + 1 < t_end) issue_tile(t_begin + 1, 1);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    if (t_begin + 1 < t_end) {
+      issue_tile(t_begin + 1, 1);
+      static_assert(2 * BPW < 16, "vmcnt immediate");
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | (2 * BPW));
+    } else {
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    }
+    asm volatile("s_barrier" ::: "memory");
   } else {
     load_tile(t_begin * BN);
     store_tile(0);
     if (t_begin + 1 < t_end) load_tile((t_begin + 1) * BN);
+    __syncthreads();
   }
-  __syncthreads();
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   uint32_t it = t_begin;
