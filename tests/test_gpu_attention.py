@@ -193,6 +193,88 @@ def test_flash_prefill_key_splits(ctx, d, hq, hkv, T, off, causal):
     assert_parity(out, ref, label=f"splits={info['splits']} T={T} off={off}")
 
 
+def _moving_max_inputs(rng, T, L, hq, hkv, d, pattern):
+    """Q/K/V whose scores move along the keys by far more than the kernels'
+    lazy-rescale thresholds (2^8 for decode, an f16 overflow of the weights
+    for prefill): every query of a GQA group leans on one direction per KV
+    head, and key j carries amp(j) times that direction, so the raw score
+    grows as amp(j) |base|^2 (up to ~6 D, i.e. 70-140 binades of weight)."""
+    g = hq // hkv
+    base = rng.standard_normal((hkv, d))
+    q = np.repeat(base[None, :, None, :], g, axis=2).reshape(1, hq, d)
+    q = q + 0.3 * rng.standard_normal((T, hq, d))
+    pos = np.arange(L) / max(L - 1, 1)
+    if pattern == "rising":
+        amp = 6.0 * pos
+    elif pattern == "falling":
+        amp = 6.0 * (1.0 - pos)
+    else:  # spikes: ~1% of the keys, anywhere, each far above the rest
+        amp = np.where(rng.random(L) < 0.01, rng.uniform(2.0, 6.0, L), 0.0)
+    k = 0.5 * rng.standard_normal((L, hkv, d)) + amp[:, None, None] * base[None]
+    v = rng.standard_normal((L, hkv, d))
+    as16 = lambda a: a.astype(np.float16).view(np.uint16)  # noqa: E731
+    return as16(q), as16(k), as16(v)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("hq,hkv,T,off,pattern", [
+    (16, 8, 1000, 300, "rising"),    # key splits
+    (64, 8, 520, 2000, "rising"),
+    (16, 8, 1000, 300, "spikes"),
+    (8, 8, 700, 37, "spikes"),
+    (16, 1, 333, 3000, "falling")])
+def test_flash_prefill_reference_max_moves(ctx, d, hq, hkv, T, off, pattern):
+    """The prefill kernels move a row's reference max only when a weight
+    overflows f16 (or the row has none yet). Scores that climb, fall or spike
+    by tens of binades along the keys make that happen in the middle of the
+    key loop, in either key half of a tile and in every key split."""
+    rng = np.random.default_rng(T + 13 * hq + d + len(pattern))
+    L = off + T
+    q, k, v = _moving_max_inputs(rng, T, L, hq, hkv, d, pattern)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+    out = run_attention(ctx, q, k, v, kind="flash-prefill", **geo)
+    ref = oracle_attention(q, k, v, **geo)
+    assert_parity(out, ref, label=f"{pattern} T={T} off={off}")
+
+
+@pytest.mark.parametrize("pattern", ["rising", "falling", "spikes"])
+@pytest.mark.parametrize("kind", ["flash-decode", "decode-split-kv"])
+def test_decode_reference_max_moves(ctx, kind, pattern):
+    """The decode kernels' lazy rescale (the reference max moves when a
+    score outgrows it by 2^8) under scores that move by tens of binades."""
+    rng = np.random.default_rng(len(kind) * 7 + len(pattern))
+    L, hq, hkv, d = 5000, 16, 8, 128
+    q, k, v = _moving_max_inputs(rng, 1, L, hq, hkv, d, pattern)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=L - 1)
+    out = run_attention(ctx, q, k, v, kind=kind, **geo)
+    assert_parity(out, oracle_attention(q, k, v, **geo), label=f"{kind} {pattern}")
+
+
+@pytest.mark.parametrize("pattern", ["rising", "spikes"])
+def test_batched_decode_reference_max_moves(ctx, pattern):
+    """The stream-K batched decode (split units merged in a second launch)
+    under scores that move by tens of binades along each sequence."""
+    rng = np.random.default_rng(91 + len(pattern))
+    B, hq, hkv, d, cap = 6, 32, 8, 128, 4000
+    lengths = [4000, 1, 2500, 3999, 700, 1800]
+    qs, ks, vs = [], [], []
+    for b in range(B):
+        q, k, v = _moving_max_inputs(rng, 1, cap, hq, hkv, d, pattern)
+        qs.append(q[0])
+        ks.append(k)
+        vs.append(v)
+    q, k, v = np.stack(qs), np.stack(ks), np.stack(vs)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    lt = ctx.tensor(np.asarray(lengths, np.uint32), mi_attn.U32)
+    batch = ctx.begin_batch()
+    out = batch.attention_decode_batched(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), lt, cfg, 0)
+    batch.finish()
+    got = ctx.download(out)
+    for b, n in enumerate(lengths):
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], ref, label=f"{pattern} sequence {b} L={n}")
+
+
 def test_c4_batched_decode_seeded(ctx):
     """B=32 sequences, lengths ~ U[1024, 8192], one launch over all of them."""
     c = workloads.case(4)
