@@ -7,8 +7,8 @@
 //    for all G query heads that share it;
 //  - S^T = K Q^T on v_mfma_f32_32x32x16_f16, K read from LDS as the A
 //    operand and Q^T kept in registers as the B operand. Each lane then holds
-//    one query row's scores, so the f32 online softmax is lane-local plus a
-//    single exchange with the partner half-wave;
+//    one query row's scores, so the f32 online softmax is lane-local (plus an
+//    exchange with the partner half-wave when the row's reference max moves);
 //  - O^T += V^T P^T on the same MFMA: P^T is the S^T accumulator converted to
 //    f16 in place (no shuffles), because V is transposed into LDS with its
 //    keys permuted (bits 2 and 3 of the key index swapped) to match the order
@@ -383,8 +383,8 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     // The reference max moves only when a weight leaves f16's range: the
     // row sum is then +inf (a weight rounded to f16 infinity) or NaN. A row
     // without a reference yet (m_run = -inf, so -mc = +inf) always lands
-    // there. Until then every weight is at most 65504 = 2^16 (1 - 2^-11)
-    // times the row's largest, O and l scaling alike, with no max pass.
+    // there. Until then every weight is at most 65504 (f16's largest finite
+    // value), and O and l share the reference, so no max pass is needed.
     weights(m_run * c2);
     if (__any(!(psum <= __FLT_MAX__))) {
       float mx = -INFINITY;
