@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import mi_attn
-from helpers import run_attention
+from helpers import assert_parity, oracle_attention, run_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -191,6 +191,39 @@ def test_captured_batched_decode_replays_match_eager(ctx):
         eager = batch.attention_decode_batched(q_in, k, v, lengths, cfg, 0)
         batch.finish()
         assert (got == ctx.download(eager)).all(), f"replay {rep}"
+    graph.destroy()
+
+
+def test_captured_split_prefill_replays_match_eager(ctx):
+    """A graph holding a FlashPrefill call that takes key splits (the pieces
+    of a row tile count their arrivals in a per-tile counter, and the last
+    one merges and sets the counter back to zero inside the launch) replays
+    with new queries, eager calls of the same kernel in between; every replay
+    equals the eager call bit for bit, and the first matches the oracle."""
+    T, hq, hkv, d, off = 1000, 16, 8, 128, 300
+    L = off + T
+    k_host, v_host = rand(60, (L, hkv, d)), rand(61, (L, hkv, d))
+    k, v = ctx.tensor(k_host), ctx.tensor(v_host)
+    q_in = ctx.empty((T, hq, d))
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, off)
+    info = ctx.plan(q_in, k, v, cfg, mi_attn.FLASH_PREFILL)
+    assert info["kernel"] == "attn_prefill" and info["splits"] > 1, info
+    capture = ctx.begin_capture()
+    out_graph = capture.attention(q_in, k, v, cfg, mi_attn.FLASH_PREFILL)
+    graph = capture.end_capture()
+    for rep in range(4):
+        q = rand(70 + rep, (T, hq, d))
+        ctx.upload(q_in, q)
+        graph.launch()
+        ctx.synchronize()
+        got = ctx.download(out_graph)
+        batch = ctx.begin_batch()
+        eager = batch.attention(q_in, k, v, cfg, mi_attn.FLASH_PREFILL)
+        batch.finish()
+        assert (got == ctx.download(eager)).all(), f"replay {rep}"
+        if rep == 0:
+            ref = oracle_attention(q, k_host, v_host, hq=hq, hkv=hkv, d=d, off=off)
+            assert_parity(got, ref, label="first replay")
     graph.destroy()
 
 
