@@ -317,8 +317,8 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     const uint16_t *v_lds = ST ? v_lds_b : v_lds_a;
 
     // S^T[key][row] for the 64 keys of the tile: two 32-key M tiles. MFMA
-    // phases run at raised wave priority, so while one wave of a SIMD feeds
-    // the matrix core the other's softmax VALU fills the issue gaps.
+    // phases run at raised wave priority (measured on MI355X, 256-row tiles:
+    // c5 2.27 ms with it, 2.33-2.35 ms without).
     __builtin_amdgcn_s_setprio(1);
     float16_t s[2];
 #pragma unroll
