@@ -40,10 +40,15 @@ __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
 // workgroup. Pass 1 sums squares (16-byte loads when rows allow), pass 2
 // writes f16(x * scale * w). Rows of up to kRmsCached 16-byte pieces per
 // lane (8192 halves) are loaded once, all pieces in flight together, and kept
-// in registers for pass 2; wider rows re-read (an L1/L2 hit).
+// in registers for pass 2; wider rows re-read (an L1/L2 hit). EARLY_W (grids
+// smaller than the CUs, a decode token) loads the weights with the row, one
+// round trip before the reduction instead of a second one after it (measured
+// on MI355X, [1, 5120]: 3.5 against 4.0 us per call); large grids keep the
+// later load, whose lower register count holds more waves per CU ([4096,
+// 5120]: 16.6 against 17.7 us).
 constexpr int kRmsCached = 16;
 
-template <bool VEC>
+template <bool VEC, bool EARLY_W>
 __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.rows) return;
@@ -53,11 +58,12 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
   float sum = 0.0f;
   if constexpr (VEC) {
     if (p.width <= 512u * kRmsCached) {
-      uint4 v[kRmsCached];
+      uint4 v[kRmsCached], wt[EARLY_W ? kRmsCached : 1];
 #pragma unroll
       for (int j = 0; j < kRmsCached; ++j) {
         const uint32_t i = lane * 8 + 512 * j;
         v[j] = i < p.width ? load16(x + i) : make_uint4(0, 0, 0, 0);
+        if constexpr (EARLY_W) wt[j] = i < p.width ? load16(p.weight + i) : make_uint4(0, 0, 0, 0);
       }
       // Same order as the streaming loop below (zero pieces add exactly 0).
 #pragma unroll
@@ -68,7 +74,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(RmsNormParams p) {
       for (int j = 0; j < kRmsCached; ++j) {
         const uint32_t i = lane * 8 + 512 * j;
         if (i < p.width) {
-          const uint4 w = load16(p.weight + i);
+          uint4 w;
+          if constexpr (EARLY_W) w = wt[j];
+          else w = load16(p.weight + i);
           const uint32_t vin[4] = {v[j].x, v[j].y, v[j].z, v[j].w}, win[4] = {w.x, w.y, w.z, w.w};
           uint32_t o[4];
 #pragma unroll
@@ -449,8 +457,9 @@ hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l) {
                    rows_vector_friendly(p.o_rows) && aligned16(p.x) && aligned16(p.out) &&
                    aligned16(p.weight);
   const dim3 grid((p.rows + 3) / 4);
-  if (vec) return dispatch(rms_norm_kernel<true>, grid, dim3(256), 0, l, p);
-  return dispatch(rms_norm_kernel<false>, grid, dim3(256), 0, l, p);
+  if (vec && grid.x < 256) return dispatch(rms_norm_kernel<true, true>, grid, dim3(256), 0, l, p);
+  if (vec) return dispatch(rms_norm_kernel<true, false>, grid, dim3(256), 0, l, p);
+  return dispatch(rms_norm_kernel<false, false>, grid, dim3(256), 0, l, p);
 }
 
 hipError_t launch_rope(const RopeParams &p, const Launch &l) {
