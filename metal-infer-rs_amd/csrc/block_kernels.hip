@@ -197,19 +197,12 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeParams p) {
   __shared__ __attribute__((aligned(16))) float s_cos[256], s_sin[256];
   const uint32_t token = blockIdx.x, tid = threadIdx.x;
   const uint32_t half = p.head_dim / 2;
-  for (uint32_t pair = tid; pair < half; pair += 256) {
-    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
-    const float angle = (float)(token + p.offset) * frequency;
-    s_cos[pair] = cosf(angle);
-    s_sin[pair] = sinf(angle);
-  }
-  __syncthreads();
   const uint32_t per_head = half / 8;
   const uint32_t items = p.heads * per_head;
   const uint16_t *xt = p.x + (int64_t)token * p.x_tok;
   uint16_t *ot = p.out + (int64_t)token * p.o_tok;
-  for (uint32_t base = 0; base < items; base += 256 * kRopeRowItems) {
-    uint4 a[kRopeRowItems], b[kRopeRowItems];
+  uint4 a[kRopeRowItems], b[kRopeRowItems];
+  auto load = [&](uint32_t base) __attribute__((always_inline)) {
 #pragma unroll
     for (uint32_t k = 0; k < kRopeRowItems; ++k) {
       const uint32_t it = base + tid + 256 * k;
@@ -219,6 +212,19 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeParams p) {
         b[k] = *reinterpret_cast<const uint4 *>(row + half);
       }
     }
+  };
+  // The first rows are in flight while the angles are computed (a decode
+  // token's rows are all of them).
+  load(0);
+  for (uint32_t pair = tid; pair < half; pair += 256) {
+    const float frequency = powf(p.theta, -(float)(pair * 2) / (float)p.head_dim);
+    const float angle = (float)(token + p.offset) * frequency;
+    s_cos[pair] = cosf(angle);
+    s_sin[pair] = sinf(angle);
+  }
+  __syncthreads();
+  for (uint32_t base = 0; base < items; base += 256 * kRopeRowItems) {
+    if (base != 0) load(base);
 #pragma unroll
     for (uint32_t k = 0; k < kRopeRowItems; ++k) {
       const uint32_t it = base + tid + 256 * k;
