@@ -206,7 +206,10 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
     return is_query ? p.q + (int64_t)token * p.q_tok + (int64_t)head * p.q_head
                     : p.k + (int64_t)token * p.k_tok + (int64_t)head * p.k_head;
   };
-  // Every row load is issued first.
+  // Every row load is issued first, the norm weights with them.
+  uint4 wv[PIECES];
+#pragma unroll
+  for (int k = 0; k < PIECES; ++k) wv[k] = *reinterpret_cast<const uint4 *>(weight + e0 + 8 * k);
   uint4 v[STEPS][PIECES];
 #pragma unroll
   for (int i = 0; i < STEPS; ++i) {
@@ -238,8 +241,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_rows_kernel(QkNormRopeParams 
   }
 #pragma unroll
   for (int k = 0; k < PIECES; ++k) {
-    const uint4 wv = *reinterpret_cast<const uint4 *>(weight + e0 + 8 * k);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t ww[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
 #pragma unroll
     for (int t = 0; t < 8; ++t) w[8 * k + t] = (t & 1) ? hi_f16(ww[t >> 1]) : lo_f16(ww[t >> 1]);
   }
