@@ -856,10 +856,19 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
 // of the reference's reduce kernels (transformer.metal:2251-2316). Recomputes
 // the stream kernel's segmentation (the key prefix sums over all sequences,
 // the segment size for p.stream_workgroups workgroups) to find the unit's
-// pieces; units held by one workgroup were written directly.
+// pieces; units held by one workgroup were written directly. One thread per
+// output element (GC x 128, at least 256, at most 1024), so the partials are
+// loaded in one pass (measured on MI355X at c4, GQA 4: 105.7 against 106.0 us
+// per call with 256 threads and two passes, bit-identical).
 template <int GC>
-__global__ __launch_bounds__(256) void attn_stream_merge_kernel(const RowsParams p) {
-  constexpr int D = 128, THREADS = 256;
+constexpr int stream_merge_threads() {
+  return GC * 128 > 1024 ? 1024 : (GC * 128 > 256 ? GC * 128 : 256);
+}
+
+template <int GC>
+__global__ __launch_bounds__(stream_merge_threads<GC>()) void attn_stream_merge_kernel(
+    const RowsParams p) {
+  constexpr int D = 128, THREADS = stream_merge_threads<GC>();
   __shared__ uint64_t s_part[2][THREADS / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t upb = p.kv_heads * p.head_chunks;
@@ -975,7 +984,8 @@ hipError_t launch_stream_gc(const RowsParams &p, RowsPhase phase, const Launch &
     return dispatch(attn_decode_stream_kernel<GC>, dim3(p.stream_workgroups),
                     dim3(kStreamWaves * 64), 0, l, p);
   const uint32_t units = p.batch * p.kv_heads * p.head_chunks;
-  return dispatch(attn_stream_merge_kernel<GC>, dim3(units), dim3(256), 0, l, p);
+  return dispatch(attn_stream_merge_kernel<GC>, dim3(units), dim3(stream_merge_threads<GC>()), 0, l,
+                  p);
 }
 
 }  // namespace
