@@ -910,9 +910,16 @@ __global__ __launch_bounds__(stream_merge_threads<GC>()) void attn_stream_merge_
 // Merges the split partials of one (row, KV head, head chunk) unit: the
 // log-sum-exp combine of the reference's reduce kernels
 // (transformer.metal:2251-2316). Launched after attn_rows_kernel on the same
-// stream, so every partial is visible without any in-kernel fence.
+// stream, so every partial is visible without any in-kernel fence. One
+// thread per output element (GC x D, at least 256, at most 1024), so the
+// partials load in one pass where the unit has at most 1024 outputs.
 template <int D, int GC>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const RowsParams p) {
+constexpr int merge_threads() {
+  return GC * D > 1024 ? 1024 : (GC * D > 256 ? GC * D : 256);
+}
+
+template <int D, int GC>
+__global__ __launch_bounds__((merge_threads<D, GC>())) void attn_merge_kernel(const RowsParams p) {
   const uint32_t unit = blockIdx.x;
   const uint32_t units_per_token = p.kv_heads * p.head_chunks;
   const uint32_t bt = unit / units_per_token;
@@ -932,7 +939,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const RowsParams p) {
   const uint32_t h0 = kvh * p.group + hc * GC;
   uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)t * p.o_tok +
                   (int64_t)h0 * p.o_head;
-  merge_splits<D, GC, 256, false>(p, unit, nsplits, out);
+  merge_splits<D, GC, merge_threads<D, GC>(), false>(p, unit, nsplits, out);
 }
 
 template <int D, int WAVES, int GC>
@@ -954,7 +961,7 @@ hipError_t launch_rows_dwg(const RowsParams &p, RowsPhase phase, const Launch &l
   }
   if (p.max_splits <= 1 || p.counters != nullptr) return no_dispatch(l);
   const uint32_t units = p.batch * p.tokens * p.kv_heads * p.head_chunks;
-  return dispatch(attn_merge_kernel<D, GC>, dim3(units), dim3(256), 0, l, p);
+  return dispatch(attn_merge_kernel<D, GC>, dim3(units), dim3(merge_threads<D, GC>()), 0, l, p);
 }
 
 template <int D, int WAVES>
