@@ -296,8 +296,10 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q,
  * fixed per-GPU buffer of 16 MiB (kept until the process ends) instead of
  * the batch arena: a call whose partials need more fails with
  * MI_ERR_RESOURCE, and its launches carry no kernel-profiling events. Every
- * call on one GPU shares that buffer, so calls that overlap on one GPU (two
- * streams, two contexts) race; calls in one stream's order are safe. */
+ * call on one GPU shares that buffer; calls in one stream's order are safe.
+ * A call from a second context while the first context's last eager call is
+ * still unfinished fails with MI_ERR_RESOURCE instead of racing it; calls
+ * recorded into graphs are not tracked, so overlapping replays race. */
 mi_status mi_attention_decode_batched_noalloc(mi_batch *batch, const mi_tensor *q,
                                               const mi_tensor *k, const mi_tensor *v,
                                               const mi_tensor *lengths,
@@ -314,10 +316,12 @@ mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx,
                                                    uint64_t length,
                                                    uint32_t *block_keys,
                                                    uint32_t *threads);
-/* MetalContext::tune_flash_decode (context.rs:269-338): times each
- * (block, threads) pair on zero-cost synthetic caches and keeps the fastest
- * per length. Runs on every device and every GQA ratio (the reference only
- * tunes on an M4 Pro with Hq == 2 * Hkv). */
+/* MetalContext::tune_flash_decode (context.rs:269-338): for each of the
+ * reference's lengths, times the library default and each of the
+ * reference's (block, threads) pairs on constant synthetic caches, and
+ * records a pair only where it beats the default by 3%; elsewhere the
+ * default stays. Runs on every device and every GQA ratio (the reference
+ * only tunes on an M4 Pro with Hq == 2 * Hkv). Replaces an earlier table. */
 mi_status mi_tune_flash_decode(mi_context *ctx, uint32_t query_heads,
                                uint32_t kv_heads, uint32_t head_dim);
 

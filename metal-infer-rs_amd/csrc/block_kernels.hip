@@ -457,13 +457,16 @@ hipError_t dispatch_matvec(const MatvecParams &p, bool vec, dim3 grid, const Lau
 
 }  // namespace
 
-hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l) {
+hipError_t launch_rms_norm(const RmsNormParams &p, uint32_t compute_units, const Launch &l) {
   if (p.rows == 0 || p.width == 0) return no_dispatch(l);
   const bool vec = p.width % 8 == 0 && rows_vector_friendly(p.x_rows) &&
                    rows_vector_friendly(p.o_rows) && aligned16(p.x) && aligned16(p.out) &&
                    aligned16(p.weight);
   const dim3 grid((p.rows + 3) / 4);
-  if (vec && grid.x < 256) return dispatch(rms_norm_kernel<true, true>, grid, dim3(256), 0, l, p);
+  // Grids smaller than the CUs load the weights with the row (one round
+  // trip less); larger ones keep the later load, which holds more waves.
+  if (vec && grid.x < compute_units)
+    return dispatch(rms_norm_kernel<true, true>, grid, dim3(256), 0, l, p);
   if (vec) return dispatch(rms_norm_kernel<true, false>, grid, dim3(256), 0, l, p);
   return dispatch(rms_norm_kernel<false, false>, grid, dim3(256), 0, l, p);
 }
@@ -493,7 +496,8 @@ hipError_t launch_rope(const RopeParams &p, const Launch &l) {
 
 bool skinny_gemm_supported(const MatvecParams &p, uint32_t compute_units) {
   auto al16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
-  return p.m > kMatvecRows && p.m <= kSkinnyMaxRows && p.n % 16 == 0 && p.n / 16 <= compute_units &&
+  return p.m > kMatvecRows && p.m <= kSkinnyMaxRows && p.n > 0 && p.k > 0 && p.n % 16 == 0 &&
+         p.n / 16 <= compute_units &&
          p.k % (4 * 2 * kSkinnyChunkSteps * 64) == 0 && p.x_row % 8 == 0 && p.w_row % 8 == 0 &&
          al16(p.x) && al16(p.w);
 }

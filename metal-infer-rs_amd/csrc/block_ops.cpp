@@ -194,8 +194,9 @@ mi_status mi_rms_norm(mi_batch *batch, const mi_tensor *input, const mi_tensor *
   p.out = static_cast<uint16_t *>(out->data);
   p.o_rows = row_index(*out);
   p.epsilon = epsilon;
+  const uint32_t cus = batch->ctx->compute_units;
   return launch(batch, "rms_norm",
-                [&](const kernels::Launch &l) { return kernels::launch_rms_norm(p, l); });
+                [&](const kernels::Launch &l) { return kernels::launch_rms_norm(p, cus, l); });
 }
 
 mi_status mi_rope(mi_batch *batch, const mi_tensor *input, uint64_t offset, float theta,
@@ -266,7 +267,9 @@ mi_status mi_matmul(mi_batch *batch, const mi_tensor *input, const mi_tensor *we
   if (kernels::skinny_gemm_supported(p, cus))
     return launch(batch, "skinny_gemm",
                   [&](const kernels::Launch &l) { return kernels::launch_skinny_gemm(p, cus, l); });
-  if (p.m > kernels::kMatvecRows) {
+  // Empty products (n or k of 0) stay on the few-row kernel: no launch for
+  // n == 0, zeros for k == 0.
+  if (p.m > kernels::kMatvecRows && p.n > 0 && p.k > 0) {
     GemmPlan *plan = nullptr;
     if ((st = gemm_plan(batch->ctx, p.m, p.n, p.k, ldx, ldw, ldo, &plan)) != MI_OK) return st;
     if (plan->ok) return run_gemm(batch, *plan, *input, *weight, *out);

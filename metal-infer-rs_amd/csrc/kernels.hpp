@@ -244,7 +244,7 @@ constexpr uint32_t kSkinnyChunkSteps = 2;  // 64-key steps per LDS chunk
 bool skinny_gemm_supported(const MatvecParams &p, uint32_t compute_units);
 hipError_t launch_skinny_gemm(const MatvecParams &p, uint32_t compute_units, const Launch &l);
 
-hipError_t launch_rms_norm(const RmsNormParams &p, const Launch &l);
+hipError_t launch_rms_norm(const RmsNormParams &p, uint32_t compute_units, const Launch &l);
 hipError_t launch_rope(const RopeParams &p, const Launch &l);
 hipError_t launch_matvec(const MatvecParams &p, const Launch &l);
 

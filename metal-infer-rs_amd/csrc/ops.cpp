@@ -75,13 +75,17 @@ uint32_t default_block(const Context *ctx, uint64_t units, uint32_t keys) {
 }
 
 // FlashDecode (block, threads) for a length (context.rs:258-267): the tuned
-// table if any (returns true), else (128, 256) — the reference's (64, 256)
-// default is an Apple-GPU choice; 128-key splits measured fastest here.
+// table's entry (returns true), else (128, 256) and false, which the planner
+// runs as the library default (8 waves, merge inside the launch). A table
+// entry with threads 0 is the tuner keeping that default for its lengths.
+// The reference's (64, 256) default is an Apple-GPU choice; 128-key splits
+// measured fastest here.
 bool flash_config_for_length(const Context *ctx, uint64_t length, uint32_t *block,
                              uint32_t *threads) {
   if (ctx != nullptr)
     for (const auto &e : ctx->flash_decode)
       if (length <= e.limit) {
+        if (e.threads == 0) break;  // the tuner kept the library default here
         *block = e.block_keys;
         *threads = e.threads;
         return true;
@@ -647,7 +651,11 @@ mi_status mi_attention_decode_batched_noalloc(mi_batch *batch, const mi_tensor *
   src.limit = kNoAllocScratchBytes;
   if (src.fixed == nullptr)
     return fail(MI_ERR_RESOURCE, "the no-allocation scratch is not set up on this device");
-  return decode_batched(batch, q, k, v, lengths, config, block_keys, out, src);
+  mi_status st = noalloc_acquire(batch->ctx, batch->capturing);
+  if (st != MI_OK) return st;
+  st = decode_batched(batch, q, k, v, lengths, config, block_keys, out, src);
+  if (st == MI_OK) noalloc_mark(batch->ctx, batch->capturing);
+  return st;
 }
 
 mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx, uint64_t length,
@@ -658,6 +666,47 @@ mi_status mi_flash_decode_configuration_for_length(const mi_context *ctx, uint64
   return MI_OK;
 }
 
+namespace {
+
+// The tuner's device buffers, freed on every path out of it.
+struct TuneBuffers {
+  mi_context *ctx;
+  mi_tensor q{}, key{}, value{}, out{};
+  ~TuneBuffers() {
+    for (mi_tensor *t : {&q, &key, &value, &out})
+      if (t->data != nullptr) mi_tensor_free(ctx, t);
+  }
+};
+
+// Median GPU time of `samples` one-call batches of FlashDecode over
+// (q, key, value), with the given (block, threads), or the library default
+// when `threads` is 0; UINT64_MAX if any call fails.
+uint64_t time_flash_decode(mi_context *ctx, const TuneBuffers &b, const mi_tensor &key,
+                           const mi_tensor &value, const mi_attention_config &cfg, uint32_t block,
+                           uint32_t threads) {
+  constexpr int kSamples = 5;
+  uint64_t samples[kSamples];
+  for (auto &sample : samples) {
+    mi_batch *batch = nullptr;
+    mi_dispatch_stats stats{};
+    if (mi_batch_begin(ctx, &batch) != MI_OK) return UINT64_MAX;
+    const mi_status st =
+        threads == 0 ? mi_attention(batch, &b.q, &key, &value, &cfg, MI_ATTN_FLASH_DECODE, &b.out)
+                     : mi_attention_flash_decode_with_configuration(batch, &b.q, &key, &value, &cfg,
+                                                                    block, threads, &b.out);
+    if (st != MI_OK) {
+      mi_batch_abandon(batch);
+      return UINT64_MAX;
+    }
+    if (mi_batch_finish(batch, &stats) != MI_OK) return UINT64_MAX;
+    sample = stats.gpu_ns;
+  }
+  std::sort(samples, samples + kSamples);
+  return samples[kSamples / 2];
+}
+
+}  // namespace
+
 mi_status mi_tune_flash_decode(mi_context *ctx, uint32_t query_heads, uint32_t kv_heads,
                                uint32_t head_dim) {
   if (ctx == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "null context");
@@ -667,63 +716,66 @@ mi_status mi_tune_flash_decode(mi_context *ctx, uint32_t query_heads, uint32_t k
   using clock = std::chrono::steady_clock;
   const auto started = clock::now();
   const auto budget = std::chrono::seconds(2);
+  // The reference's lengths and (block, threads) candidates and 2 s budget
+  // (context.rs:269-338), plus the library default (threads 0: 8 waves, the
+  // split merge inside the launch), which every candidate has to beat by
+  // kMargin to replace it. A length the budget leaves untimed keeps the
+  // default, so tuning never selects a slower path than no tuning.
   const uint64_t lengths[] = {512, 640, 1024, 2048, 4096, 8192};
   const uint64_t maximum = 8192;
   const uint32_t candidates[8][2] = {{64, 256}, {32, 256},  {128, 256}, {256, 256},
                                      {64, 128}, {32, 128}, {128, 128}, {256, 128}};
-  int64_t qshape[3] = {1, query_heads, head_dim};
-  int64_t cshape[3] = {(int64_t)maximum, kv_heads, head_dim};
-  mi_tensor q, key, value, out;
+  constexpr double kMargin = 0.97;
+  const int64_t qshape[3] = {1, query_heads, head_dim};
+  const int64_t cshape[3] = {(int64_t)maximum, kv_heads, head_dim};
+  TuneBuffers b{ctx};
   mi_status st;
-  if ((st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &q)) != MI_OK) return st;
-  if ((st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &key)) != MI_OK) return st;
-  if ((st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &value)) != MI_OK) return st;
-  if ((st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &out)) != MI_OK) return st;
+  if ((st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &b.q)) != MI_OK ||
+      (st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &b.key)) != MI_OK ||
+      (st = mi_tensor_empty(ctx, cshape, 3, MI_F16, &b.value)) != MI_OK ||
+      (st = mi_tensor_empty(ctx, qshape, 3, MI_F16, &b.out)) != MI_OK)
+    return st;
   // 1.0 queries and 0.5 cache entries (context.rs:282-287).
-  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(q.data), 0x3c00, element_count(q));
-  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(key.data), 0x3800, element_count(key));
-  (void)hipMemsetD16(reinterpret_cast<hipDeviceptr_t>(value.data), 0x3800, element_count(value));
-  (void)hipDeviceSynchronize();
+  hipError_t err = hipSuccess;
+  const std::pair<const mi_tensor *, unsigned short> fills[] = {
+      {&b.q, 0x3c00}, {&b.key, 0x3800}, {&b.value, 0x3800}};
+  for (const auto &[t, bits] : fills)
+    if (err == hipSuccess)
+      err = hipMemsetD16Async(reinterpret_cast<hipDeviceptr_t>(t->data), bits, element_count(*t),
+                              ctx->stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+  if (err != hipSuccess)
+    return fail(MI_ERR_COMMAND, std::string("flash decode tuning inputs: ") + hipGetErrorString(err));
+  // Time against the untuned library (a table from an earlier call would
+  // redirect the default candidate).
+  ctx->flash_decode.clear();
   std::vector<FlashDecodeEntry> chosen;
   for (uint64_t length : lengths) {
     if (clock::now() - started >= budget) break;
     mi_tensor k_prefix, v_prefix;
-    mi_tensor_prefix(&key, (int64_t)length, &k_prefix);
-    mi_tensor_prefix(&value, (int64_t)length, &v_prefix);
-    mi_attention_config cfg{query_heads, kv_heads, head_dim, 1, (uint32_t)(length - 1)};
+    if (mi_tensor_prefix(&b.key, (int64_t)length, &k_prefix) != MI_OK ||
+        mi_tensor_prefix(&b.value, (int64_t)length, &v_prefix) != MI_OK)
+      break;
+    const mi_attention_config cfg{query_heads, kv_heads, head_dim, 1, (uint32_t)(length - 1)};
+    const uint64_t default_ns = time_flash_decode(ctx, b, k_prefix, v_prefix, cfg, 0, 0);
     uint64_t best_ns = UINT64_MAX;
-    uint32_t best_block = 64, best_threads = 256;
+    uint32_t best_block = 0, best_threads = 0;
     for (const auto &cand : candidates) {
       if (clock::now() - started >= budget) break;
-      uint64_t samples[3];
-      bool ok = true;
-      for (auto &sample : samples) {
-        mi_batch *batch = nullptr;
-        mi_dispatch_stats stats{};
-        if (mi_batch_begin(ctx, &batch) != MI_OK) { ok = false; break; }
-        if (mi_attention_flash_decode_with_configuration(batch, &q, &k_prefix, &v_prefix, &cfg,
-                                                         cand[0], cand[1], &out) != MI_OK) {
-          mi_batch_abandon(batch);
-          ok = false;
-          break;
-        }
-        if (mi_batch_finish(batch, &stats) != MI_OK) { ok = false; break; }
-        sample = stats.gpu_ns;
-      }
-      if (!ok) continue;
-      std::sort(samples, samples + 3);
-      if (samples[1] < best_ns) {
-        best_ns = samples[1];
+      const uint64_t ns = time_flash_decode(ctx, b, k_prefix, v_prefix, cfg, cand[0], cand[1]);
+      if (ns < best_ns) {
+        best_ns = ns;
         best_block = cand[0];
         best_threads = cand[1];
       }
     }
-    chosen.push_back({length, best_block, best_threads});
+    if (default_ns == UINT64_MAX || best_ns == UINT64_MAX ||
+        (double)best_ns >= kMargin * (double)default_ns)
+      chosen.push_back({length, 0, 0});  // the library default
+    else
+      chosen.push_back({length, best_block, best_threads});
   }
-  mi_tensor_free(ctx, &q);
-  mi_tensor_free(ctx, &key);
-  mi_tensor_free(ctx, &value);
-  mi_tensor_free(ctx, &out);
+  // Lengths past the last timed one keep the default too.
   ctx->flash_decode = chosen;
   clear_error();
   return MI_OK;

@@ -261,6 +261,10 @@ mi_status mi_context_create(int32_t device, mi_context **out) {
   ctx->allocated += counters * sizeof(uint32_t);
   // The no-allocation entry point's fixed scratch on this device.
   mi_status st = noalloc_init(device);
+  if (st == MI_OK) {
+    err = hipEventCreateWithFlags(&ctx->noalloc_done, hipEventDisableTiming);
+    if (err != hipSuccess) st = hip_fail(MI_ERR_RESOURCE, "no-allocation event", err);
+  }
   if (st != MI_OK) {
     hipFree(ctx->split_counters);
     hipStreamDestroy(ctx->stream);
@@ -290,6 +294,8 @@ void mi_context_destroy(mi_context *ctx) {
   }
   hipFree(ctx->split_counters);
   mi::release_gemm(ctx);
+  mi::noalloc_forget(ctx);
+  if (ctx->noalloc_done != nullptr) hipEventDestroy(ctx->noalloc_done);
   hipStreamDestroy(ctx->stream);
   delete ctx;
 }

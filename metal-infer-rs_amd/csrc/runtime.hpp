@@ -61,6 +61,8 @@ struct Lease {
 constexpr size_t kScratchChunkBytes = 32ull << 20;
 constexpr size_t kScratchAlignment = 256;
 
+// One row of the tuned FlashDecode table: lengths up to `limit` run with
+// (block_keys, threads); threads == 0 keeps the library default there.
 struct FlashDecodeEntry {
   uint64_t limit;
   uint32_t block_keys;
@@ -92,6 +94,8 @@ struct Context {
   // hipBLASLt handle and per-shape GEMM plans, made at the first matmul
   // with more rows than the few-row kernel takes.
   GemmState *gemm = nullptr;
+  // Recorded on `stream` after each eager no-allocation call.
+  hipEvent_t noalloc_done = nullptr;
 };
 
 // Frees the context's hipBLASLt handle and plans (after its stream drained).
@@ -141,6 +145,14 @@ void scratch_give(Context *ctx, const ScratchSource &src, void *ptr);
 constexpr size_t kNoAllocScratchBytes = 16ull << 20;
 mi_status noalloc_init(int device);
 void *noalloc_scratch(int device);
+// Cross-context use of that array: noalloc_acquire fails with
+// MI_ERR_RESOURCE while another context's last eager call is unfinished,
+// else makes `ctx` its user; noalloc_mark records ctx's completion event
+// after its launches (skipped under capture); noalloc_forget drops a
+// destroyed context.
+mi_status noalloc_acquire(Context *ctx, bool capturing);
+void noalloc_mark(Context *ctx, bool capturing);
+void noalloc_forget(const Context *ctx);
 
 
 // Launches through `fn` on the batch stream. With kernel profiling on, the

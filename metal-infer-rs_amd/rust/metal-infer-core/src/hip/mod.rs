@@ -17,9 +17,15 @@
 //!   the device with logical [capacity, Hkv, D] views.
 //! A status maps back onto `CoreError` one to one (error.rs:5-32); the
 //! message comes from `mi_last_error()`.
+//!
+//! Lifetimes: the library context is held by a reference-counted handle that
+//! every tensor, arena lease, cache and clone of `HipContext` shares, so
+//! `mi_context_destroy` runs only after the last of them has dropped (a
+//! tensor outliving its `HipContext` still frees into a live context).
 #![allow(clippy::missing_safety_doc)]
 
 pub mod ffi;
+pub mod types;
 
 use std::ffi::CStr;
 use std::marker::PhantomData;
@@ -30,7 +36,8 @@ use std::time::Duration;
 use half::f16;
 
 use self::ffi::*;
-use crate::{AttentionConfig, AttentionKind, CoreError, DType, QkNormRopeCacheConfig};
+use self::types::{AttentionConfig, AttentionKind, DType, QkNormRopeCacheConfig};
+use crate::CoreError;
 
 /// DispatchStats (context.rs:31-35).
 #[derive(Clone, Copy, Debug, Default)]
@@ -97,8 +104,9 @@ fn parse_length_error(message: &str) -> CoreError {
     CoreError::DataLength { expected: number("expected "), actual: number(" has ") }
 }
 
-/// mi_status -> CoreError. HIP has no NSError to carry, so the Metal-specific
-/// Shader / Pipeline / Command payloads become the message-carrying variants.
+/// mi_status -> CoreError, one variant per status. On this target the
+/// Shader / Pipeline / Command variants carry the HIP runtime's message
+/// (`BackendError` is `String` off macOS).
 fn check(status: mi_status) -> Result<(), CoreError> {
     if status == MI_OK {
         return Ok(());
@@ -107,8 +115,11 @@ fn check(status: mi_status) -> Result<(), CoreError> {
     Err(match status {
         MI_ERR_NO_DEVICE => CoreError::NoDevice,
         MI_ERR_RESOURCE => CoreError::Resource("HIP device memory or stream"),
-        MI_ERR_SHADER | MI_ERR_PIPELINE | MI_ERR_MISSING_KERNEL => CoreError::MissingKernel(message),
-        MI_ERR_COMMAND | MI_ERR_UNKNOWN_COMMAND => CoreError::UnknownCommand,
+        MI_ERR_SHADER => CoreError::Shader(message),
+        MI_ERR_PIPELINE => CoreError::Pipeline(message),
+        MI_ERR_MISSING_KERNEL => CoreError::MissingKernel(message),
+        MI_ERR_COMMAND => CoreError::Command(message),
+        MI_ERR_UNKNOWN_COMMAND => CoreError::UnknownCommand,
         MI_ERR_DTYPE => parse_dtype_error(&message),
         MI_ERR_DATA_LENGTH => parse_length_error(&message),
         MI_ERR_PROFILING => CoreError::Profiling(message),
@@ -160,17 +171,28 @@ fn qk_config(config: QkNormRopeCacheConfig) -> Result<mi_qk_norm_rope_cache_conf
     })
 }
 
+/// The library context, destroyed when its last holder drops.
+struct ContextHandle {
+    raw: *mut mi_context,
+}
+
+impl Drop for ContextHandle {
+    fn drop(&mut self) {
+        unsafe { mi_context_destroy(self.raw) }
+    }
+}
+
 /// Device memory from mi_tensor_empty, freed when the last Tensor using it
 /// drops.
 struct Allocation {
-    ctx: *mut mi_context,
+    ctx: Rc<ContextHandle>,
     desc: mi_tensor,
 }
 
 impl Drop for Allocation {
     fn drop(&mut self) {
         unsafe {
-            mi_tensor_free(self.ctx, &mut self.desc);
+            mi_tensor_free(self.ctx.raw, &mut self.desc);
         }
     }
 }
@@ -179,14 +201,14 @@ impl Drop for Allocation {
 /// returned to the arena when the last Tensor using it drops, which may be
 /// after the batch was waited on.
 struct Lease {
-    ctx: *mut mi_context,
+    ctx: Rc<ContextHandle>,
     desc: mi_tensor,
 }
 
 impl Drop for Lease {
     fn drop(&mut self) {
         unsafe {
-            mi_scratch_release(self.ctx, &self.desc);
+            mi_scratch_release(self.ctx.raw, &self.desc);
         }
     }
 }
@@ -195,6 +217,8 @@ impl Drop for Lease {
 /// view of it have dropped.
 struct CacheStorage {
     raw: *mut mi_kv_cache,
+    // Declared after `raw`, so the cache is destroyed before the context.
+    _ctx: Rc<ContextHandle>,
 }
 
 impl Drop for CacheStorage {
@@ -209,7 +233,7 @@ impl Drop for CacheStorage {
 #[derive(Clone)]
 pub struct Tensor {
     pub(crate) desc: mi_tensor,
-    ctx: *mut mi_context,
+    ctx: Rc<ContextHandle>,
     shape: Vec<usize>,
     allocation: Option<Rc<Allocation>>,
     lease: Option<Rc<Lease>>,
@@ -228,13 +252,13 @@ impl std::fmt::Debug for Tensor {
 }
 
 impl Tensor {
-    fn from_desc(ctx: *mut mi_context, desc: mi_tensor) -> Self {
+    fn from_desc(ctx: Rc<ContextHandle>, desc: mi_tensor) -> Self {
         let shape = (0..desc.rank as usize).map(|i| desc.shape[i] as usize).collect();
         Self { desc, ctx, shape, allocation: None, lease: None, cache: None }
     }
 
     fn view(&self, desc: mi_tensor) -> Self {
-        let mut view = Self::from_desc(self.ctx, desc);
+        let mut view = Self::from_desc(self.ctx.clone(), desc);
         view.allocation = self.allocation.clone();
         view.lease = self.lease.clone();
         view.cache = self.cache.clone();
@@ -286,7 +310,7 @@ impl Tensor {
         }
         let mut host = vec![0_u16; self.len()];
         check(unsafe {
-            mi_tensor_download(self.ctx, &self.desc, host.as_mut_ptr().cast(), host.len() * 2)
+            mi_tensor_download(self.ctx.raw, &self.desc, host.as_mut_ptr().cast(), host.len() * 2)
         })?;
         Ok(host)
     }
@@ -303,7 +327,7 @@ impl Tensor {
         }
         let mut host = vec![0_u32; self.len()];
         check(unsafe {
-            mi_tensor_download(self.ctx, &self.desc, host.as_mut_ptr().cast(), host.len() * 4)
+            mi_tensor_download(self.ctx.raw, &self.desc, host.as_mut_ptr().cast(), host.len() * 4)
         })?;
         Ok(host)
     }
@@ -311,15 +335,12 @@ impl Tensor {
 
 /// MetalContext counterpart over one HIP device: one in-order stream, the
 /// kernels, per-batch scratch arenas. Single-threaded, like MetalContext
-/// (the raw pointer keeps it !Send and !Sync).
+/// (`Rc` and the raw pointer keep it !Send and !Sync); clones share the
+/// device context, as MetalContext clones do (qwen3.rs:224).
+#[derive(Clone)]
 pub struct HipContext {
+    handle: Rc<ContextHandle>,
     raw: *mut mi_context,
-}
-
-impl Drop for HipContext {
-    fn drop(&mut self) {
-        unsafe { mi_context_destroy(self.raw) }
-    }
 }
 
 impl HipContext {
@@ -334,7 +355,7 @@ impl HipContext {
         }
         let mut raw = ptr::null_mut();
         check(unsafe { mi_context_create(device, &mut raw) })?;
-        Ok(Self { raw })
+        Ok(Self { handle: Rc::new(ContextHandle { raw }), raw })
     }
 
     pub fn device_name(&self) -> String {
@@ -421,8 +442,8 @@ impl HipContext {
             mi_tensor_empty(self.raw, dims.as_ptr(), dims.len() as i32, dtype_code(dtype),
                             &mut desc)
         })?;
-        let mut tensor = Tensor::from_desc(self.raw, desc);
-        tensor.allocation = Some(Rc::new(Allocation { ctx: self.raw, desc }));
+        let mut tensor = Tensor::from_desc(self.handle.clone(), desc);
+        tensor.allocation = Some(Rc::new(Allocation { ctx: self.handle.clone(), desc }));
         Ok(tensor)
     }
 
@@ -451,6 +472,62 @@ impl HipContext {
         let tensor = self.empty(shape, DType::U32)?;
         self.upload(&tensor, values)?;
         Ok(tensor)
+    }
+
+    /// One operation in its own batch, waited on (the eager mirrors of
+    /// ops.rs:131-218). The result's arena lease outlives the batch.
+    fn immediate<T>(&self, operation: impl FnOnce(&mut CommandBatch<'_>) -> Result<T, CoreError>)
+        -> Result<T, CoreError> {
+        let mut batch = self.begin_batch()?;
+        let result = operation(&mut batch)?;
+        batch.finish()?;
+        Ok(result)
+    }
+
+    /// ops.rs:131-137.
+    pub fn matmul(&self, input: &Tensor, weight: &Tensor) -> Result<Tensor, CoreError> {
+        self.immediate(|batch| batch.matmul(input, weight))
+    }
+
+    /// ops.rs:139-146.
+    pub fn rms_norm(&self, input: &Tensor, weight: &Tensor, epsilon: f32)
+        -> Result<Tensor, CoreError> {
+        self.immediate(|batch| batch.rms_norm(input, weight, epsilon))
+    }
+
+    /// ops.rs:164-171.
+    pub fn rope(&self, input: &Tensor, offset: usize, theta: f32) -> Result<Tensor, CoreError> {
+        self.immediate(|batch| batch.rope(input, offset, theta))
+    }
+
+    /// ops.rs:173-182.
+    pub fn attention(&self, query: &Tensor, key: &Tensor, value: &Tensor,
+                     config: AttentionConfig, kind: AttentionKind) -> Result<Tensor, CoreError> {
+        self.immediate(|batch| batch.attention(query, key, value, config, kind))
+    }
+
+    /// ops.rs:184-193: the reference's 256-thread configuration.
+    pub fn attention_flash_decode_with_block(&self, query: &Tensor, key: &Tensor,
+                                             value: &Tensor, config: AttentionConfig,
+                                             block_keys: usize) -> Result<Tensor, CoreError> {
+        self.attention_flash_decode_with_configuration(query, key, value, config, block_keys, 256)
+    }
+
+    /// ops.rs:195-209.
+    pub fn attention_flash_decode_with_configuration(&self, query: &Tensor, key: &Tensor,
+                                                     value: &Tensor, config: AttentionConfig,
+                                                     block_keys: usize, threads: usize)
+        -> Result<Tensor, CoreError> {
+        self.immediate(|batch| {
+            batch.attention_flash_decode_with_configuration(query, key, value, config, block_keys,
+                                                            threads)
+        })
+    }
+
+    /// ops.rs:211-218.
+    pub fn copy_into_cache(&self, source: &Tensor, cache: &Tensor, offset: usize)
+        -> Result<(), CoreError> {
+        self.immediate(|batch| batch.copy_into_cache(source, cache, offset))
     }
 }
 
@@ -483,8 +560,8 @@ impl<'context> CommandBatch<'context> {
         check(unsafe {
             mi_batch_empty(self.raw, dims.as_ptr(), dims.len() as i32, dtype_code(dtype), &mut desc)
         })?;
-        let mut tensor = Tensor::from_desc(self.context.raw, desc);
-        tensor.lease = Some(Rc::new(Lease { ctx: self.context.raw, desc }));
+        let mut tensor = Tensor::from_desc(self.context.handle.clone(), desc);
+        tensor.lease = Some(Rc::new(Lease { ctx: self.context.handle.clone(), desc }));
         Ok(tensor)
     }
 
@@ -718,7 +795,7 @@ impl Drop for Graph<'_> {
 /// logical [capacity, Hkv, D] views (LayerCache, qwen3.rs:36-40) that keep
 /// the storage alive.
 pub struct HipKvCache {
-    ctx: *mut mi_context,
+    ctx: Rc<ContextHandle>,
     storage: Rc<CacheStorage>,
 }
 
@@ -730,7 +807,8 @@ impl HipKvCache {
             mi_kv_cache_create(context.raw, layers as u32, kv_heads as u32, head_dim as u32,
                                capacity as u64, &mut raw)
         })?;
-        Ok(Self { ctx: context.raw, storage: Rc::new(CacheStorage { raw }) })
+        let storage = Rc::new(CacheStorage { raw, _ctx: context.handle.clone() });
+        Ok(Self { ctx: context.handle.clone(), storage })
     }
 
     pub fn len(&self) -> usize {
@@ -761,8 +839,8 @@ impl HipKvCache {
         let mut key = unsafe { std::mem::zeroed::<mi_tensor>() };
         let mut value = unsafe { std::mem::zeroed::<mi_tensor>() };
         check(unsafe { mi_kv_cache_layer(self.storage.raw, index as u32, &mut key, &mut value) })?;
-        let mut key = Tensor::from_desc(self.ctx, key);
-        let mut value = Tensor::from_desc(self.ctx, value);
+        let mut key = Tensor::from_desc(self.ctx.clone(), key);
+        let mut value = Tensor::from_desc(self.ctx.clone(), value);
         key.cache = Some(self.storage.clone());
         value.cache = Some(self.storage.clone());
         Ok((key, value))

@@ -247,6 +247,20 @@ def test_matmul_strided_views(ctx, m):
     assert (full[:, :32] == 0).all()
 
 
+def test_matmul_empty_products(ctx):
+    """Skinny-range row counts (16) with an empty product: n == 0 launches
+    nothing and succeeds, k == 0 writes zeros. Views of real storage, so no
+    zero-byte allocation is involved."""
+    x_dev = ctx.tensor(rand(90, (16, 64)))
+    w_dev = ctx.tensor(rand(91, (32, 64)))
+    out_dev = ctx.tensor(np.full((16, 32), 0x3C00, dtype=np.uint16))  # 1.0 everywhere
+    batch = ctx.begin_batch()
+    batch.matmul(x_dev, w_dev.view((0, 64), (64, 1)), out=out_dev.view((16, 0), (32, 1)))
+    batch.matmul(x_dev.view((16, 0), (64, 1)), w_dev.view((32, 0), (64, 1)), out=out_dev)
+    batch.finish()
+    assert (ctx.download(out_dev) == 0).all()
+
+
 def test_matmul_errors(ctx):
     x = ctx.tensor(rand(1, (2, 3)))
     w = ctx.tensor(rand(2, (5, 4)))

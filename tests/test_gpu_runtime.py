@@ -109,15 +109,75 @@ def test_allocated_bytes_tracks_tensors(ctx):
     assert ctx.allocated_bytes() == before
 
 
-def test_tuned_flash_decode_table_is_used(ctx):
-    ctx.tune_flash_decode(16, 8, 128)
-    for length in (512, 2048, 8192):
-        block, threads = ctx.flash_decode_configuration_for_length(length)
-        assert block in (32, 64, 128, 256) and threads in (128, 256)
-    rng_q = rand(7, (1, 16, 128))
-    k, v = rand(8, (700, 8, 128)), rand(9, (700, 8, 128))
-    out = run_attention(ctx, rng_q, k, v, kind="flash-decode", hq=16, hkv=8, d=128, off=699)
-    assert out.shape == (1, 16, 128)
+def _flash_decode_us(context, q, k, v, cfg, calls=20):
+    """GPU time of one FlashDecode dispatch: a batch of `calls` dispatches."""
+    batch = context.begin_batch()
+    for _ in range(calls):
+        batch.attention(q, k, v, cfg, mi_attn.FLASH_DECODE)
+    return batch.finish().gpu_ns / calls / 1e3
+
+
+def test_tuned_flash_decode_is_never_slower_than_the_default(ctx):
+    """Qwen3Model::load tunes FlashDecode at load time (qwen3.rs:218). The
+    tuner keeps the library default unless a reference (block, threads) pair
+    beats it, so a tuned context runs c2-shaped decode no slower than an
+    untuned one, with the oracle's output. A fresh context is tuned; the
+    session context stays untuned."""
+    L, hq, hkv, d = 2048, 16, 8, 128
+    q, k, v = rand(21, (1, hq, d)), rand(22, (L, hkv, d)), rand(23, (L, hkv, d))
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, L - 1)
+    fresh = mi_attn.Context(0)
+    try:
+        fresh.tune_flash_decode(hq, hkv, d)
+        for length in (512, 2048, 8192):
+            block, threads = fresh.flash_decode_configuration_for_length(length)
+            assert block in (32, 64, 128, 256) and threads in (128, 256)
+        args_a = (ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), cfg)
+        args_b = (fresh.tensor(q), fresh.tensor(k), fresh.tensor(v), cfg)
+        untuned_plan = ctx.plan(*args_a, mi_attn.FLASH_DECODE)
+        tuned_plan = fresh.plan(*args_b, mi_attn.FLASH_DECODE)
+        out = fresh.download(fresh.attention(*args_b, mi_attn.FLASH_DECODE))
+        assert_parity(out, oracle_attention(q, k, v, hq=hq, hkv=hkv, d=d, off=L - 1))
+        _flash_decode_us(ctx, *args_a)
+        _flash_decode_us(fresh, *args_b)
+        untuned, tuned = [], []
+        for _ in range(7):
+            untuned.append(_flash_decode_us(ctx, *args_a))
+            tuned.append(_flash_decode_us(fresh, *args_b))
+        ratio = float(np.median(tuned) / np.median(untuned))
+        print(f"[tune] untuned {np.median(untuned):.2f} us {untuned_plan}, "
+              f"tuned {np.median(tuned):.2f} us {tuned_plan}, ratio {ratio:.3f}", flush=True)
+        if tuned_plan == untuned_plan:
+            # the same kernel and grid: only the timing noise differs
+            assert (out == ctx.download(ctx.attention(*args_a, mi_attn.FLASH_DECODE))).all()
+            assert ratio <= 1.10, ratio
+        else:
+            assert ratio <= 1.02, ratio
+        # the session context kept the untuned default
+        assert ctx.plan(*args_a, mi_attn.FLASH_DECODE) == untuned_plan
+    finally:
+        fresh.close()
+
+
+def test_tuning_keeps_the_default_where_it_wins(ctx):
+    """A tuned table entry that kept the default (threads 0 internally)
+    plans exactly as an untuned context does, and the tuned table is still
+    used for explicit lengths of the table (a 700-key decode)."""
+    fresh = mi_attn.Context(0)
+    try:
+        fresh.tune_flash_decode(16, 8, 128)
+        q, k, v = rand(7, (1, 16, 128)), rand(8, (700, 8, 128)), rand(9, (700, 8, 128))
+        cfg = mi_attn.AttentionConfig(16, 8, 128, True, 699)
+        args = (fresh.tensor(q), fresh.tensor(k), fresh.tensor(v), cfg)
+        tuned = fresh.plan(*args, mi_attn.FLASH_DECODE)
+        block, threads = fresh.flash_decode_configuration_for_length(700)
+        explicit = fresh.plan(*args, mi_attn.FLASH_DECODE, block, threads)
+        default = ctx.plan(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), cfg, mi_attn.FLASH_DECODE)
+        assert tuned in (default, explicit), (tuned, default, explicit)
+        out = fresh.download(fresh.attention(*args, mi_attn.FLASH_DECODE))
+        assert_parity(out, oracle_attention(q, k, v, hq=16, hkv=8, d=128, off=699))
+    finally:
+        fresh.close()
 
 
 # ------------------------------------------------- captured decode steps --

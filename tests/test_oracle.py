@@ -89,6 +89,42 @@ def test_xorshift_matches_marsaglias_published_xor64():
     assert first == (8748534153485358512 * 0xFFFFFFFF) >> 64
 
 
+def test_box_muller_known_answers_from_marsaglias_seed():
+    """The normal generator's Box-Muller step as the input spec states it
+    (cos branch, u1 replaced by 1 - u1, f64 -> f32 -> f16 RNE), from
+    Marsaglia's published xor64 states: draw 0 uses the published first two
+    states exactly, later draws the states a Python xor64 gives (checked
+    against the third published state). numpy's float64 log/cos and its
+    float16 cast are independent of the oracle's C. The sin branch, u1 in
+    place of 1 - u1, and swapped uniforms each give different bits here."""
+    mask = (1 << 64) - 1
+
+    def step(x):
+        x ^= (x << 13) & mask
+        x ^= x >> 7
+        x ^= (x << 17) & mask
+        return x
+
+    states, x = [], 88172645463325252
+    for _ in range(16):
+        x = step(x)
+        states.append(x)
+    assert states[:3] == [8748534153485358512, 3040900993826735515, 3453997556048239312]
+    u = np.array(states, dtype=np.float64) / 2.0**64
+    u1, u2 = u[0::2], u[1::2]
+
+    def spec(a, b, trig=np.cos, flip=True):
+        radius = np.sqrt(-2.0 * np.log(1.0 - a if flip else a))
+        return (radius * trig(2.0 * np.pi * b)).astype(np.float32).astype(np.float16)
+
+    expected = spec(u1, u2).view(np.uint16)
+    got = oracle.normal_f16(88172645463325252, (8,), threads=1)
+    assert (got == expected).all(), (got, expected)
+    assert (workloads.normal_f16(88172645463325252, 8, threads=1) == expected).all()
+    for wrong in (spec(u1, u2, trig=np.sin), spec(u1, u2, flip=False), spec(u2, u1)):
+        assert (wrong.view(np.uint16) != expected).any()
+
+
 def test_xorshift_jump_composes():
     s = oracle.lib().orc_xorshift_seed(12345)
     assert oracle.xorshift_jump(s, 1000 + 2345) == oracle.xorshift_jump(

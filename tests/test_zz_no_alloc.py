@@ -126,3 +126,32 @@ def test_no_alloc_rejects_partials_beyond_its_buffer(nctx):
     # one key per sequence: the output is that key's value row, per head
     expect = np.repeat(kv[:, 0], hq // hkv, axis=1)
     assert (got == expect).all()
+
+
+def test_no_alloc_two_contexts_alternating(nctx):
+    """Two contexts on one GPU share the fixed buffer. Calls that alternate
+    in stream order (each waited on before the other context calls) both
+    succeed and equal the arena entry point bit for bit: the second context
+    takes the buffer over once the first one's call has finished."""
+    other = mi_attn.Context(0)
+    try:
+        rng = np.random.default_rng(17)
+        B, hq, hkv, d, cap = 6, 32, 8, 128, 1500
+        lengths = [1500, 3, 777, 1024, 64, 1299]
+        q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
+        k = [rng.standard_normal((cap, hkv, d)).astype(np.float16).view(np.uint16)
+             for _ in range(B)]
+        v = [rng.standard_normal((cap, hkv, d)).astype(np.float16).view(np.uint16)
+             for _ in range(B)]
+        cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+        views = {id(c): _cache(c, k, v, lengths, cap) for c in (nctx, other)}
+        for rep in range(2):
+            for context in (nctx, other):
+                _, _, kview, vview = views[id(context)]
+                ref, got = _both(context, q, kview, vview, lengths, cfg, 0)
+                assert (got == ref).all(), f"round {rep}: the two entry points differ"
+        for context in (nctx, other):
+            kt, vt, _, _ = views[id(context)]
+            kt.free(), vt.free()
+    finally:
+        other.close()
