@@ -16,7 +16,12 @@ roofline; `accuracy` is the max-abs error of the timed call's output against
 the CPU oracle, computed in the cpu_baseline leg from the oracle runs it
 times (null with --no-cpu).
 
+`compare` holds the reference's attention compare harness
+(`metal-infer-bench attention --kind compare`) at its default decode shape and
+one prefill shape; `--compare` runs only that harness, at a chosen shape.
+
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --compare [--tokens 1] [--length 640] [--iterations 50]
 """
 from __future__ import annotations
 
@@ -537,6 +542,211 @@ def bench_o_proj(ctx, hip, eager) -> list[dict]:
     return results
 
 
+# ---------------------------------------------------------------- floors --
+
+def probe_lib() -> ctypes.CDLL:
+    """libmi_probe.so (include/mi_probe.h): calibration kernels."""
+    lib = ctypes.CDLL(str(ROOT / "metal-infer-rs_amd" / "libmi_probe.so"))
+    vp, u32, u64, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32
+    lib.mi_probe_empty.argtypes = [vp, u32, u32, u32]
+    lib.mi_probe_read.argtypes = [vp, vp, u64, u32, vp]
+    lib.mi_probe_split_decode.argtypes = [vp, vp, vp, u64, u32, u32, u32, u32, i32, vp, vp, vp,
+                                          vp]
+    for fn in (lib.mi_probe_empty, lib.mi_probe_read, lib.mi_probe_split_decode):
+        fn.restype = i32
+    return lib
+
+
+def bench_floors(ctx, hip, steps) -> dict:
+    """What the decode kernels' time is made of, measured beside them in the
+    same process with the same timing (HIP graph replays on the library's
+    stream):
+     - c2 (single-sequence FlashDecode, 64 rotated caches): an empty kernel
+       on the attention kernel's grid (16 splits x 8 KV heads, 512 threads);
+       the same grid loading exactly the attention kernel's K/V rows (the
+       data phase); the data phase plus the split exchange (partials with
+       device-scope stores, release arrival, last-arriver acquire and merge,
+       f16 output); and the attention call itself;
+     - c4: a streaming read of c4's algorithmic bytes by 512 to 2048
+       workgroups (the achievable HBM read rate at that size), beside the
+       batched-decode call."""
+    probe = probe_lib()
+    out = {}
+    c = workloads.case(2)
+    hq, hkv, d, L = c.q_heads, c.kv_heads, c.head_dim, c.kv_length
+    group, block = hq // hkv, 128
+    splits = (L + block - 1) // block
+    log(f"floors: c2 grid {splits} x {hkv}, {ROTATE} rotated caches")
+    cache = ctx.kv_cache(ROTATE, hkv, d, L)
+    layers = [cache.layer(i) for i in range(ROTATE)]
+    for key, value in layers:
+        ctx.upload(key, c.k)
+        ctx.upload(value, c.v)
+    head_stride = layers[0][0].strides[1]
+    partial = ctx.empty((hkv * splits * group * (d + 2),), mi_attn.F32)
+    counters = ctx.tensor(np.zeros(hkv, np.uint32), mi_attn.U32)
+    words = ctx.empty((hkv * splits,), mi_attn.U32)
+    out16 = ctx.empty((hkv * group * d,))
+    q = ctx.tensor(c.q)
+    attn_out = ctx.empty(c.q.shape)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, c.query_offset)
+
+    def split_probe(publish):
+        def enqueue(batch, i):
+            key, value = layers[i % ROTATE]
+            rc = probe.mi_probe_split_decode(batch.stream, key.data_ptr, value.data_ptr,
+                                             head_stride, hkv, group, L, block, publish,
+                                             partial.data_ptr, counters.data_ptr,
+                                             words.data_ptr, out16.data_ptr)
+            hip.check(rc, "mi_probe_split_decode")
+        return enqueue
+
+    def empty(batch, i):
+        hip.check(probe.mi_probe_empty(batch.stream, splits, hkv, 512), "mi_probe_empty")
+
+    def attention(batch, i):
+        key, value = layers[i % ROTATE]
+        return batch.attention(q, key, value, cfg, mi_attn.FLASH_DECODE, out=attn_out)
+
+    calls = max(ROTATE, (steps + ROTATE - 1) // ROTATE * ROTATE)
+    c2 = {"grid": [splits, hkv], "threads": 512, "calls": calls}
+    for label, enqueue in (("empty_kernel", empty), ("data_phase", split_probe(0)),
+                           ("data_publish_merge", split_probe(1)), ("attention", attention)):
+        reps = [timed(ctx, hip, enqueue, calls, 2, False) for _ in range(3)]
+        c2[label + "_us"] = round(float(np.median(reps)) * 1e6, 3)
+    assert (ctx.download(counters) == 0).all(), "the probe left a counter set"
+    log("floors c2: " + ", ".join(f"{k} {v}" for k, v in c2.items() if k.endswith("_us")))
+    out["c2"] = c2
+    for t in (partial, counters, words, out16, q, attn_out):
+        t.free()
+    cache.close()
+
+    c4 = workloads.case(4, generate=False)
+    nbytes = c4.algorithmic_bytes()
+    # per-workgroup shares are rounded up to 16 bytes: at most 16 B more per workgroup
+    src = ctx.empty((nbytes // 2 + 32 * 1024,))
+    sink = ctx.empty((2048 * 4,), mi_attn.U32)
+    rates = {}
+    for wgs in (512, 1024, 2048):
+        per = (nbytes + wgs - 1) // wgs
+        per = (per + 15) // 16 * 16
+
+        def read(batch, i, per=per, wgs=wgs):
+            hip.check(probe.mi_probe_read(batch.stream, src.data_ptr, per, wgs, sink.data_ptr),
+                      "mi_probe_read")
+        seconds = timed(ctx, hip, read, steps, 2, False)
+        rates[str(wgs)] = round(per * wgs / seconds / 1e9, 1)
+    out["c4_read"] = {"bytes": nbytes, "gb_per_s_by_workgroups": rates,
+                      "best_gb_per_s": max(rates.values())}
+    log(f"floors c4 read: {rates} GB/s")
+    src.free()
+    sink.free()
+    return out
+
+
+# ------------------------------------------------------ compare harness --
+
+def duration_stats(samples_s: list[float]) -> tuple[float, float, float]:
+    """(mean, median, p95) in ms, indexed as bench.rs:1995-2008 does
+    (median = sorted[n / 2], p95 = sorted[round((n - 1) * 0.95)])."""
+    s = sorted(samples_s)
+    p95 = s[int(round((len(s) - 1) * 0.95))]
+    return (sum(s) / len(s) * 1e3, s[len(s) // 2] * 1e3, p95 * 1e3)
+
+
+def compare_attention(ctx, tokens=1, length=640, query_heads=16, kv_heads=8, head_dim=128,
+                      iterations=50, warmup=10) -> dict:
+    """`metal-infer-bench attention --kind compare`
+    (crates/metal-infer-cli/src/bin/bench.rs:927-1108): every attention kind
+    on the closed-form inputs (bench.rs:973-981), each timed as `iterations`
+    one-dispatch batches after `warmup` (begin_batch, attention, finish:
+    wall clock around the three calls, GPU time from the batch's events;
+    bench.rs:823-836), reported as mean / median / p95 with the max-abs
+    error of its output against the Reference kind's (bench.rs:1243-1252).
+    FlashDecode appears as the reference's two explicit (64, 256) and
+    (64, 128) configurations and as this library's default (what
+    `attention(.., FlashDecode)` runs untuned); it is offered for every GQA
+    ratio (the reference requires two query heads per KV head)."""
+    if not (0 < tokens <= length) or min(query_heads, kv_heads, head_dim) <= 0:
+        raise ValueError("attention dimensions must be non-zero and tokens must not exceed length")
+    if query_heads % kv_heads:
+        raise ValueError("attention query-heads must be divisible by kv-heads")
+    qh, kh, vh = workloads.compare_inputs(tokens, length, query_heads, kv_heads, head_dim)
+    q, k, v = ctx.tensor(qh), ctx.tensor(kh), ctx.tensor(vh)
+    cfg = mi_attn.AttentionConfig(query_heads, kv_heads, head_dim, True, length - tokens)
+
+    def f32(bits):
+        return bits.view(np.float16).astype(np.float32)
+
+    def variant(name, dispatch):
+        batch = ctx.begin_batch()
+        out = dispatch(batch)
+        batch.finish()
+        got = f32(ctx.download(out))
+        del out
+        for _ in range(warmup):
+            batch = ctx.begin_batch()
+            dispatch(batch)
+            batch.finish()
+        wall, gpu = [], []
+        for _ in range(iterations):
+            t0 = time.perf_counter()
+            batch = ctx.begin_batch()
+            dispatch(batch)
+            stats = batch.finish()
+            wall.append(time.perf_counter() - t0)
+            gpu.append(stats.gpu_ns * 1e-9)
+        w, g = duration_stats(wall), duration_stats(gpu)
+        return got, {"kind": name, "wall_mean_ms": w[0], "wall_median_ms": w[1],
+                     "wall_p95_ms": w[2], "gpu_mean_ms": g[0], "gpu_median_ms": g[1],
+                     "gpu_p95_ms": g[2]}
+
+    def kind(attention_kind):
+        return lambda batch: batch.attention(q, k, v, cfg, attention_kind)
+
+    reference_out, reference = variant("reference", kind(mi_attn.REFERENCE))
+    reference["max_abs_error"] = 0.0
+    comparison = {"reference": reference}
+
+    def add(key, name, dispatch):
+        out, report = variant(name, dispatch)
+        report["max_abs_error"] = float(np.abs(out - reference_out).max())
+        comparison[key] = report
+
+    add("tiled", "tiled", kind(mi_attn.TILED))
+    if tokens > 1:
+        add("flash_prefill", "flash-prefill", kind(mi_attn.FLASH_PREFILL))
+    else:
+        add("decode_split_kv", "decode-split-kv", kind(mi_attn.DECODE_SPLIT_KV))
+        add("flash_decode", "flash-decode-256t",
+            lambda b: b.attention_flash_decode_with_configuration(q, k, v, cfg, 64, 256))
+        add("flash_decode_128", "flash-decode-128t",
+            lambda b: b.attention_flash_decode_with_configuration(q, k, v, cfg, 64, 128))
+        add("flash_decode_default", "flash-decode", kind(mi_attn.FLASH_DECODE))
+    # The variant the model's policy would pick (bench.rs:1050-1063, with this
+    # library's default FlashDecode standing for the (64, 256) one).
+    if tokens == 1:
+        selected = comparison["flash_decode_default" if length >= 256 else "decode_split_kv"]
+    else:
+        selected = comparison["flash_prefill" if tokens >= 32 else "tiled"]
+    for t in (q, k, v):
+        t.free()
+    return {"benchmark": f"attention_f16[tokens={tokens},length={length}]",
+            "device": ctx.device_name, "iterations": iterations, "warmup": warmup,
+            "shape": {"query_heads": query_heads, "kv_heads": kv_heads, "head_dim": head_dim,
+                      "query_offset": length - tokens},
+            "selected": selected["kind"],
+            "mean_ms": selected["wall_mean_ms"], "median_ms": selected["wall_median_ms"],
+            "p95_ms": selected["wall_p95_ms"], "gpu_mean_ms": selected["gpu_mean_ms"],
+            "gpu_median_ms": selected["gpu_median_ms"], "gpu_p95_ms": selected["gpu_p95_ms"],
+            "allocated_bytes": ctx.allocated_bytes(), "attention_comparison": comparison}
+
+
+# The compare block of the default run: the harness's defaults (one decode
+# token over 640 keys, Qwen3-0.6B heads) and one prefill shape.
+COMPARE_SHAPES = ((1, 640), (640, 640))
+
+
 # -------------------------------------------------------------- CPU leg ---
 
 def host_cpu() -> dict:
@@ -640,14 +850,26 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workloads", default="c4,c5,c3,c2,c1,step,o_proj",
+    ap.add_argument("--workloads", default="c4,c5,c3,c2,c1,step,o_proj,compare",
                     help="comma list of c4 (headline), c5, c3, c2, c1, step (decode step "
-                         "graphs), o_proj (with the other neighbours); profiling runs "
-                         "select one at a time")
+                         "graphs), o_proj (with the other neighbours), compare (the "
+                         "attention compare harness), floors (calibration kernels beside "
+                         "the decodes); profiling runs select one at a time")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of HIP graph replays (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB KV copy (PMC traffic calibration)")
+    ap.add_argument("--compare", action="store_true",
+                    help="only the attention compare harness (metal-infer-bench attention "
+                         "--kind compare) at --tokens/--length/--query-heads/--kv-heads/"
+                         "--head-dim, --iterations/--compare-warmup; prints its report")
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--length", type=int, default=640)
+    ap.add_argument("--query-heads", type=int, default=16)
+    ap.add_argument("--kv-heads", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--iterations", type=int, default=50)
+    ap.add_argument("--compare-warmup", type=int, default=10)
     ap.add_argument("--no-dispatch-events", action="store_true",
                     help="skip the eager per-dispatch event pass beside each timed region "
                          "(for a profiler trace of the timed calls only)")
@@ -662,7 +884,7 @@ def main() -> int:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
-    unknown = set(chosen) - {"c1", "c2", "c3", "c4", "c5", "step", "o_proj"}
+    unknown = set(chosen) - {"c1", "c2", "c3", "c4", "c5", "step", "o_proj", "compare", "floors"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -670,6 +892,15 @@ def main() -> int:
     hip = Hip()
     ctx = mi_attn.Context(0)
     log(f"device: {ctx.device_name}, {ctx.compute_units} CUs")
+    if args.compare:
+        if args.iterations < 1:
+            print("--iterations must be >= 1", file=sys.stderr)
+            return 2
+        print(json.dumps(compare_attention(ctx, args.tokens, args.length, args.query_heads,
+                                           args.kv_heads, args.head_dim, args.iterations,
+                                           args.compare_warmup)), flush=True)
+        ctx.close()
+        return 0
     timing = "eager launches" if args.eager else "HIP graph replay"
     K, W = args.steps, args.warmup
     result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": K,
@@ -736,6 +967,16 @@ def main() -> int:
     if "o_proj" in chosen:
         result["o_proj"] = bench_o_proj(ctx, hip, args.eager)
         result["neighbours"] = bench_neighbours(ctx, hip, args.eager)
+    if "floors" in chosen and not args.eager:
+        result["floors"] = bench_floors(ctx, hip, 64)
+    if "compare" in chosen:
+        result["compare"] = []
+        for tokens, length in COMPARE_SHAPES:
+            report = compare_attention(ctx, tokens, length)
+            log(f"compare {report['benchmark']}: " + ", ".join(
+                f"{r['kind']} {r['gpu_median_ms'] * 1e3:.1f} us (err {r['max_abs_error']:.1e})"
+                for r in report["attention_comparison"].values()))
+            result["compare"].append(report)
     if args.copy_calibration:
         result["copy_calibration"] = copy_calibration(ctx, hip)
     if not args.no_cpu and checked:

@@ -59,6 +59,25 @@ def config_seed(config: int) -> int:
     return 0x4D490000 + 16 * config
 
 
+def compare_inputs(tokens: int, length: int, q_heads: int, kv_heads: int,
+                   head_dim: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """The attention bench's closed-form inputs
+    (crates/metal-infer-cli/src/bin/bench.rs:973-981): over the flat index i,
+    Q = (i % 43) / 43 - 0.5, K = (i % 37) / 37 - 0.25, V = (i % 29) / 29, in
+    f32 and then rounded to f16 (round to nearest even, as tensor_f16 does).
+    Returns f16 bits shaped [T, Hq, D], [L, Hkv, D], [L, Hkv, D]."""
+    f = np.float32
+
+    def pattern(n, mod, offset):
+        i = np.arange(n, dtype=np.int64)
+        return ((i % mod).astype(f) / f(mod) - f(offset)).astype(np.float16).view(np.uint16)
+
+    q = pattern(tokens * q_heads * head_dim, 43, 0.5).reshape(tokens, q_heads, head_dim)
+    k = pattern(length * kv_heads * head_dim, 37, 0.25).reshape(length, kv_heads, head_dim)
+    v = pattern(length * kv_heads * head_dim, 29, 0.0).reshape(length, kv_heads, head_dim)
+    return q, k, v
+
+
 @dataclass
 class AttentionCase:
     """One BASELINE configuration (1-based index `config`)."""

@@ -307,3 +307,26 @@ def test_prefill_needs_non_negative_position_strides():
     assert plan(q, huge, fwd, cfg, FLASH_PREFILL)["kernel"] == "attn_rows"
     near = tensor((L, hkv, d), strides=((1 << 25) - 1024, d, 1))
     assert plan(q, near, fwd, cfg, FLASH_PREFILL)["kernel"] == "attn_prefill"
+
+
+def test_probe_library_exports_its_header():
+    """libmi_probe.so (calibration kernels, include/mi_probe.h) is separate
+    from the attention library, which exports none of its symbols."""
+    path = ROOT / "metal-infer-rs_amd" / "libmi_probe.so"
+    names = declared("mi_probe.h")
+    assert names == ["mi_probe_empty", "mi_probe_read", "mi_probe_split_decode"]
+    assert set(names) <= exported(path)
+    assert not set(names) & exported(ROOT / "metal-infer-rs_amd" / "libmi_attn.so")
+
+
+def test_compare_statistics_follow_the_reference_indexing():
+    """bench.rs:1995-2008: median = sorted[n / 2], p95 = sorted[round((n - 1)
+    * 0.95)], mean over all samples, in ms."""
+    import bench
+
+    samples = [i * 1e-3 for i in (5, 1, 4, 2, 3, 10, 9, 8, 7, 6)]
+    mean, median, p95 = bench.duration_stats(samples)
+    assert mean == pytest.approx(5.5)
+    assert median == pytest.approx(6.0)   # sorted[5]
+    assert p95 == pytest.approx(10.0)     # sorted[round(8.55)] = sorted[9]
+    assert bench.duration_stats([2e-3])[1:] == pytest.approx((2.0, 2.0))
