@@ -4,6 +4,13 @@
       Markdown table of a `rocprofv3 --kernel-trace --stats --output-format csv`
       run: calls and average / min / max duration per kernel (and, with --last,
       the average of each kernel's last N dispatches, in trace order).
+  counters --run WORKLOAD=DIR[,DIR...] ... --command CMD [--skip N]
+      SQ / GRBM counters of each workload's dominant kernel from
+      `rocprofv3 --pmc` passes (per-dispatch means after the first N dispatches)
+      and what they imply: the shader clock (GRBM_GUI_ACTIVE over the XCDs and
+      the dispatch's duration), the MFMA pipes' busy share of SIMD cycles
+      (SQ_VALU_MFMA_BUSY_CYCLES over SIMDs x GRBM cycles), and the same against
+      the 2.4 GHz peak clock.
   traffic --copy-bytes N --run WORKLOAD=FETCH_DIR,WRITE_DIR ... --command CMD
       HBM bytes per dispatch of each workload's dominant kernel from two
       `rocprofv3 --pmc` passes (FETCH_SIZE, then WRITE_SIZE; KiB per
@@ -156,6 +163,82 @@ def traffic(args) -> None:
         f.write("\n".join(lines) + "\n")
 
 
+# MI355X: 256 CUs of 4 SIMDs in 8 XCDs; GRBM_GUI_ACTIVE is summed over the
+# XCDs. Peak clock of the dense MFMA rating (2.5 PFLOP/s f16).
+XCDS, SIMDS, PEAK_HZ = 8, 1024, 2.4e9
+
+
+def counters(args) -> None:
+    out = {"source": "rocprofv3 --pmc, per-dispatch means", "command": args.command,
+           "workloads": {}}
+    lines = []
+    for spec in args.run:
+        workload, dirs = spec.split("=", 1)
+        record, kernels = DOMINANT[workload]
+        values: dict[str, list[float]] = defaultdict(list)
+        durations: list[float] = []
+        for directory in dirs.split(","):
+            seen: dict[str, int] = defaultdict(int)
+            rows = sorted(csv.DictReader(one_file(directory, "counter_collection.csv").open()),
+                          key=lambda r: int(r["Dispatch_Id"]))
+            for r in rows:
+                if base(r["Kernel_Name"]) != kernels[0]:
+                    continue
+                seen[r["Counter_Name"]] += 1
+                if seen[r["Counter_Name"]] <= args.skip:
+                    continue
+                values[r["Counter_Name"]].append(float(r["Counter_Value"]))
+                if r["Counter_Name"] == "GRBM_GUI_ACTIVE":
+                    durations.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e9)
+        mean = {k: sum(v) / len(v) for k, v in values.items()}
+        entry = {"kernel": kernels[0], "dispatches": len(durations),
+                 "counters": {k: round(v, 1) for k, v in sorted(mean.items())}}
+        if "GRBM_GUI_ACTIVE" in mean and durations:
+            seconds = sum(durations) / len(durations)
+            cycles = mean["GRBM_GUI_ACTIVE"] / XCDS
+            entry["duration_us"] = round(seconds * 1e6, 2)
+            entry["clock_ghz"] = round(cycles / seconds / 1e9, 3)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                busy = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / SIMDS
+                entry["mfma_busy_of_cycles"] = round(busy / cycles, 4)
+                entry["mfma_busy_of_peak_clock"] = round(busy / (seconds * PEAK_HZ), 4)
+        if "SQ_INSTS_MFMA" in mean and "SQ_INSTS_VALU" in mean:
+            entry["valu_per_mfma"] = round(mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"], 3)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                entry["busy_cycles_per_mfma"] = round(
+                    mean["SQ_VALU_MFMA_BUSY_CYCLES"] / mean["SQ_INSTS_MFMA"], 2)
+        out["workloads"][workload] = entry
+        lines.append(f"| {workload} | `{kernels[0]}` | {entry['dispatches']} | "
+                     f"{entry.get('duration_us', '—')} | {entry.get('clock_ghz', '—')} | "
+                     f"{entry.get('mfma_busy_of_cycles', '—')} | "
+                     f"{entry.get('mfma_busy_of_peak_clock', '—')} | "
+                     f"{entry.get('valu_per_mfma', '—')} |")
+    Path(args.json).write_text(json.dumps(out, indent=1) + "\n")
+    with open(args.md, "w") as f:
+        f.write(f"# {args.title}\n\n" if args.title else "# SQ / GRBM counters\n\n")
+        f.write("Per-dispatch means of `rocprofv3 --pmc` passes (the first "
+                f"{args.skip} dispatches of each counter skipped as warmup). MI355X: "
+                f"{SIMDS} SIMDs in {XCDS} XCDs; GRBM_GUI_ACTIVE is summed over the XCDs, so "
+                "clock = GRBM_GUI_ACTIVE / 8 / duration, and the MFMA busy share = "
+                "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (GRBM_GUI_ACTIVE / 8). Against "
+                "the 2.4 GHz clock of the 2.5 PFLOP/s rating the same busy cycles are "
+                "divided by duration x 2.4 GHz.\n\nCommands (from the repository root on "
+                "the GPU box):\n\n")
+        for c in args.command.split(" ;; "):
+            f.write(f"    {c}\n")
+        f.write("\n| workload | kernel | dispatches | duration (us) | clock (GHz) | "
+                "MFMA busy / cycles | MFMA busy / peak-clock cycles | VALU per MFMA |\n")
+        f.write("|---|---|---:|---:|---:|---:|---:|---:|\n")
+        f.write("\n".join(lines) + "\n\n## Counter means per dispatch\n\n")
+        names = sorted({k for e in out["workloads"].values() for k in e["counters"]})
+        f.write("| counter | " + " | ".join(out["workloads"]) + " |\n")
+        f.write("|---|" + "---:|" * len(out["workloads"]) + "\n")
+        for n in names:
+            f.write(f"| {n} | " + " | ".join(
+                f"{e['counters'].get(n, float('nan')):.4g}" for e in out["workloads"].values())
+                + " |\n")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -171,8 +254,15 @@ def main() -> None:
     t.add_argument("--command", required=True)
     t.add_argument("--json", required=True)
     t.add_argument("--md", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--run", action="append", required=True)
+    c.add_argument("--command", required=True)
+    c.add_argument("--skip", type=int, default=2)
+    c.add_argument("--title", default="")
+    c.add_argument("--json", required=True)
+    c.add_argument("--md", required=True)
     args = ap.parse_args()
-    stats(args) if args.cmd == "stats" else traffic(args)
+    {"stats": stats, "traffic": traffic, "counters": counters}[args.cmd](args)
 
 
 if __name__ == "__main__":
