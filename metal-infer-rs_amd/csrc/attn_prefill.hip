@@ -117,19 +117,13 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   // Dispatch order: workgroups are handed out in linear-id order, and
   // round-robin over the 8 XCDs, so id % 8 selects the XCD. When the KV
   // heads split evenly over the XCDs, each XCD gets whole heads (their K/V
-  // stay in its L2). Within a head, row tiles go heaviest first and the key
-  // splits of one row tile go together.
-  // Row tile t's key tiles: the causal window of its last row.
-  auto key_tiles = [&](uint32_t t) -> uint32_t {
-    const uint32_t last = min(p.tokens - 1, ((t + 1) * BM - 1) / p.group);
-    const uint64_t k = p.causal != 0 ? min((uint64_t)p.kv_length, (uint64_t)p.query_offset + last + 1)
-                                     : (uint64_t)p.kv_length;
-    return (uint32_t)((k + BN - 1) / BN);
-  };
+  // stay in its L2). Within a head, row tiles go heaviest first and the
+  // gridDim.z key splits of one row tile go together; a split past the row
+  // tile's last key tile returns at once.
   uint32_t tile, kvh, split;
   {
     const uint32_t id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const uint32_t H = p.kv_heads;
+    const uint32_t H = p.kv_heads, S = gridDim.z;
     uint32_t rest;
     if (H % 8 == 0) {
       const uint32_t xcd = id % 8, k = id / 8, per = H / 8;
@@ -139,22 +133,8 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       kvh = id % H;
       rest = id / H;
     }
-    if (p.pieces_per_head == 0) {
-      tile = p.row_tiles - 1 - rest;
-      split = 0;
-    } else {
-      // Key splits: the grid holds only the non-empty pieces, p.pieces_per_head
-      // per KV head; piece `rest` of the head, counting from the heaviest
-      // row tile down (so every piece starts in the launch's first wave).
-      tile = p.row_tiles - 1;
-      uint32_t pieces = (key_tiles(tile) + p.split_tiles - 1) / p.split_tiles;
-      while (rest >= pieces && tile > 0) {
-        rest -= pieces;
-        --tile;
-        pieces = (key_tiles(tile) + p.split_tiles - 1) / p.split_tiles;
-      }
-      split = rest;
-    }
+    tile = p.row_tiles - 1 - rest / S;
+    split = rest % S;
   }
   const uint32_t row0 = tile * BM;
   const uint32_t my_row = row0 + wave * 32 + n;
@@ -632,10 +612,8 @@ bool prefill_supported(uint32_t head_dim) {
 }
 
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
-  // Unsplit: one workgroup per (row tile, KV head); split: one per non-empty
-  // (row tile, KV head, key split) piece.
-  const dim3 grid = p.pieces_per_head != 0 ? dim3(p.pieces_per_head * p.kv_heads)
-                                           : dim3(p.row_tiles, p.kv_heads);
+  // One workgroup per (row tile, KV head, key split).
+  const dim3 grid(p.row_tiles, p.kv_heads, p.splits > 1 ? p.splits : 1);
   switch (head_dim) {
     case 64:
       if (p.block_m != 128) return hipErrorInvalidValue;

@@ -147,23 +147,26 @@ __device__ __forceinline__ float2 load_coherent2(const float *ptr) {
 constexpr int kWaitVmcnt0 = 0x0F70;
 
 // Split partials passed between workgroups of one launch ("the last split
-// to arrive merges"). The protocol, in HIP memory-model terms:
-//  - every thread stores its part of the partial (store_partial*), waits for
-//    its stores, and the workgroup meets at a barrier (workgroup-scope
-//    synchronisation);
-//  - one thread counts the arrival with an agent-scope RELEASE
-//    read-modify-write (arrive), which orders all of the workgroup's stores
-//    before the count at device scope;
+// to arrive merges"):
+//  - every thread stores its part of the partial with agent-scope atomic
+//    stores (store_partial*), waits for them to complete (s_waitcnt
+//    vmcnt(0)), and the workgroup meets at a barrier;
+//  - one thread counts the arrival with an agent-scope read-modify-write on
+//    the unit's counter (arrive);
 //  - the thread that sees itself last issues an agent-scope ACQUIRE fence
 //    (acquire_partials), then the workgroup meets at a barrier and reads the
-//    other splits' partials (load_partial*).
-// Release then acquire through the counter makes every partial visible to
-// the merging workgroup, on whatever XCD each split ran. On gfx950 the
-// release is an L2 writeback of the arriving workgroup's XCD and the acquire
-// an L2 invalidate. The partials are device-scope (write-through) stores, so
-// the writeback finds them already written: measured on MI355X, the release
-// with write-through stores cost less than with plain stores (c2 8.67 against
-// 9.1 us per call, the relaxed protocol without fences 8.45 us).
+//    other splits' partials with agent-scope atomic loads (load_partial*).
+// The arrival carries no release fence. On gfx950 (the HIP memory model as
+// LLVM implements it for gfx942 and later) an agent-scope release is an L2
+// writeback (buffer_wbl2 sc1) followed by s_waitcnt vmcnt(0). The writeback
+// is there for plain stores, which may sit dirty in the writer's XCD L2;
+// everything published here is written with agent-scope atomic stores
+// (sc1: written through to the device-coherent level), and the writer has
+// already waited for their completion before it arrives, so the writeback
+// would only flush unrelated lines. Measured on MI355X (same box, c3
+// prefill with 3 key splits): 42.2-42.6 us per call with the release, 39.3-
+// 40.0 us without it and with the acquire kept, 39.0-39.5 us with neither.
+// The merger's acquire (an L2 invalidate) is cheap and is kept.
 __device__ __forceinline__ void store_partial(float *ptr, float v) { store_coherent(ptr, v); }
 __device__ __forceinline__ void store_partial2(float *ptr, float a, float b) {
   store_coherent2(ptr, a, b);
@@ -172,9 +175,10 @@ __device__ __forceinline__ float load_partial(const float *ptr) {
   return __hip_atomic_load(const_cast<float *>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float2 load_partial2(const float *ptr) { return load_coherent2(ptr); }
-// Returns the counter's previous value.
+// Returns the counter's previous value. Call after the workgroup's partial
+// stores have completed (s_waitcnt vmcnt(0)) and it has met at a barrier.
 __device__ __forceinline__ uint32_t arrive(uint32_t *counter) {
-  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void acquire_partials() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");

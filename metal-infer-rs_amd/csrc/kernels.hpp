@@ -152,9 +152,6 @@ struct PrefillParams {
   uint32_t *counters;
   uint32_t split_tiles;
   uint32_t splits;
-  // Non-empty pieces per KV head when split (0: unsplit); the launch has
-  // exactly pieces_per_head * kv_heads workgroups, heaviest row tiles first.
-  uint32_t pieces_per_head;
 };
 
 // Split pass (one workgroup per key block; writes the output directly when a
@@ -261,8 +258,8 @@ constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim
 bool prefill_supported(uint32_t head_dim);
 // 128-row prefill workgroups resident per CU: two, or one at head_dim 256.
 constexpr uint32_t prefill_workgroups_per_cu(uint32_t head_dim) { return head_dim == 256 ? 1 : 2; }
-// One launch, split merges included: grid (row_tiles, kv_heads), or the
-// pieces_per_head * kv_heads non-empty pieces when the keys are split.
+// One launch, split merges included: grid (row_tiles, kv_heads, splits);
+// a key split past its row tile's last key tile returns at once.
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
 // Capacity of a context's split-K arrival counters (row tiles x KV heads of
 // a split prefill grid).

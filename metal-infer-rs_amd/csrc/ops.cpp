@@ -28,7 +28,6 @@ struct AttnPlan {
   uint32_t grid[3] = {0, 0, 0};
   uint32_t threads = 0;
   uint32_t block_m = kernels::kPrefillBlockM;  // prefill: packed rows per workgroup
-  uint64_t pieces = 0;           // prefill key splits: non-empty pieces per KV head
   const char *kernel = "";
 };
 
@@ -164,7 +163,6 @@ void plan_prefill_splits(const Context *ctx, AttnPlan *p, bool causal, uint32_t 
     for (uint32_t n : tiles) pieces += ceil_div(n, per_split);
     if (splits < 2 || pieces * p->grid[1] > cus) continue;
     p->splits = splits;
-    p->pieces = pieces;
     p->block_keys = per_split * kernels::kPrefillBlockN;
     p->grid[2] = splits;
     p->scratch_bytes = (uint64_t)splits * wgs * (block_m / 32) * kernels::kPrefillPartialSlots(p->D) * 64 *
@@ -270,27 +268,18 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
     plan_prefill_splits(ctx, &p, config->causal != 0, config->query_offset,
                         kernels::kPrefillBlockM, kernels::prefill_workgroups_per_cu(p.D));
     // The 8-wave row tile (256 rows, one workgroup per CU) shares each K/V
-    // tile between twice the rows. Grids of at least four such workgroups per
-    // CU take it (measured on MI355X: c5 +3%; c3 unsplit, 128 such
-    // workgroups, 30% slower). So does a D = 128 grid that takes key splits,
-    // when its split at one workgroup per CU is no coarser: c3 keeps 3 x 11
-    // tiles in 256 pieces instead of 504 and ran 6% faster (42.7-43.6 against
-    // 44.8-47.6 us, bit-identical output).
+    // tile between twice the rows. Unsplit grids of at least four such
+    // workgroups per CU take it (measured on MI355X: c5 +3%; c3 unsplit, 128
+    // such workgroups, 30% slower). Grids that take key splits keep the
+    // 128-row tile at two workgroups per CU: c3 (3 x 11 key tiles, 504
+    // non-empty pieces in a grid of 768) ran 36.2-38.6 us per call against
+    // 38.9-39.5 us with 256-row tiles (256 pieces, one per CU), same box.
     const uint64_t cus = std::max<uint32_t>(ctx ? ctx->compute_units : 256, 1);
     const uint64_t big_tiles = ceil_div((uint64_t)p.T * p.G, kernels::kPrefillBlockM2);
     if (p.splits == 1 && p.D == 128 && big_tiles * p.Hkv >= 4 * cus) {
       p.block_m = kernels::kPrefillBlockM2;
       p.threads = 512;
       p.grid[0] = (uint32_t)big_tiles;
-    } else if (p.splits > 1 && p.D == 128) {
-      AttnPlan big = p;
-      big.block_m = kernels::kPrefillBlockM2;
-      big.threads = 512;
-      big.grid[0] = (uint32_t)big_tiles;
-      big.grid[2] = 1;
-      plan_prefill_splits(ctx, &big, config->causal != 0, config->query_offset,
-                          kernels::kPrefillBlockM2, 1);
-      if (big.splits > 1 && big.block_keys <= p.block_keys) p = big;
     }
     *plan = p;
     return MI_OK;
@@ -399,7 +388,6 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     pp.scale_log2 = scale * log2e;
     pp.splits = p.splits;
     pp.split_tiles = p.splits > 1 ? p.block_keys / kernels::kPrefillBlockN : 0;
-    pp.pieces_per_head = p.splits > 1 ? (uint32_t)p.pieces : 0;
     void *scratch = nullptr;
     mi_status st;
     if (p.splits > 1) {

@@ -233,12 +233,11 @@ def test_flash_prefill_routes_to_mfma_kernel():
     q = tensor((2048, 64, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
     assert p["grid"][:2] == (128, 8) and p["block_threads"] == 256
-    # c3: 2048 x 2 = 4096 packed rows. It takes key splits, and at one 8-wave
-    # workgroup per CU its split is no coarser than with 128-row tiles at two
-    # per CU: 16 row tiles of 256 rows per KV head.
+    # c3: 2048 x 2 = 4096 packed rows. It takes key splits, which keep the
+    # 128-row tile at two workgroups per CU: 32 row tiles per KV head.
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
-    assert p["grid"][:2] == (16, 8) and p["block_threads"] == 512, p
+    assert p["grid"][:2] == (32, 8) and p["block_threads"] == 256, p
 
 
 def _pieces(T, G, L, off, per_split_keys, block_m=128):
@@ -254,22 +253,17 @@ def _pieces(T, G, L, off, per_split_keys, block_m=128):
 def test_small_prefill_grids_split_the_keys():
     # c3: 256 workgroups of 128 rows on 256 CUs. The split count is the largest
     # whose non-empty pieces all fit at two workgroups per CU: 3 splits of 11
-    # key tiles. With 256-row tiles at one workgroup per CU the largest such
-    # split is the same 3 x 11 tiles, so the plan takes the 256-row tile
-    # (16 row tiles per KV head, 32 pieces each).
+    # key tiles, 504 non-empty pieces in a grid of 32 x 8 x 3.
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
-    assert p["grid"] == (16, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
-    assert p["block_threads"] == 512
-    # (m, l) + 128 O values per row as f32, for 256 rows (8 waves) per row tile
-    assert p["scratch_bytes"] == 3 * 16 * 8 * 8 * (1 + 128 // 4) * 64 * 2 * 4
+    assert p["grid"] == (32, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
+    assert p["block_threads"] == 256
+    # (m, l) + 128 O values per row as f32, for 128 rows (4 waves) per row tile
+    assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 4) * 64 * 2 * 4
     pieces, max_tiles = _pieces(2048, 2, 2048, 0, p["block_keys"])
-    assert pieces * 8 <= 2 * 256
+    assert pieces == 63 and pieces * 8 <= 2 * 256
     finer = -(-max_tiles // 4) * 64  # one more split would not fit
     assert _pieces(2048, 2, 2048, 0, finer)[0] * 8 > 2 * 256
-    big_pieces, big_max = _pieces(2048, 2, 2048, 0, p["block_keys"], block_m=256)
-    assert big_pieces * 8 <= 256 and big_max == max_tiles == 32
-    assert _pieces(2048, 2, 2048, 0, finer, block_m=256)[0] * 8 > 256
     # c5 fills the chip on its own: no split, no scratch
     q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
