@@ -42,7 +42,7 @@ int32_t mi_probe_read(void *stream, const void *src, uint64_t bytes_per_workgrou
  *  - publish != 0: each workgroup stores a (max, sum, acc[128]) partial for
  *    each of the `group` query heads of its KV head into `partial` (unit x
  *    split x group x 130 floats) with device-scope stores, waits for them,
- *    counts its arrival on counters[kv head] with an agent-scope release,
+ *    counts its arrival on counters[kv head] with an agent-scope atomic add,
  *    and the last split to arrive acquires, resets the counter to zero and
  *    merges every split's partial (one load per split per output element)
  *    into out_f16 [group x 128 halves per KV head] — the attention kernel's
