@@ -170,15 +170,23 @@ DISPATCH_EVENTS = True  # --no-dispatch-events clears it
 
 
 def kernel_profile(ctx: mi_attn.Context, enqueue, count: int,
-                   workload: str = "") -> tuple[str, float, dict]:
+                   workload: str = "", warm: int = 0) -> tuple[str, float, dict]:
     """The dominant kernel (largest total time) of `count` eager calls, its
     median duration per launch (s), and every kernel's median, from the
     start / stop events the library binds to each dispatch on the batch's
-    stream (hipExtLaunchKernelGGL). A diagnostic beside the timed region;
-    skipped with --no-dispatch-events (so that a profiler's trace of the run
-    holds only the timed calls)."""
+    stream (hipExtLaunchKernelGGL). `warm` unprofiled calls run first: the
+    first dispatches of a power-capped kernel after the GPU idled (c5 after
+    its output's download) run up to ~10% slower than the steady state the
+    timed replay sees. A diagnostic beside the timed region; skipped with
+    --no-dispatch-events (so that a profiler's trace of the run holds only
+    the timed calls)."""
     if not DISPATCH_EVENTS and workload in DOMINANT:
         return DOMINANT[workload], float("nan"), {}
+    if warm:
+        batch = ctx.begin_batch()
+        keep = [enqueue(batch, i) for i in range(warm)]
+        batch.finish()
+        del keep
     ctx.take_kernel_profiles()
     ctx.set_kernel_profiling(True)
     try:
@@ -393,12 +401,59 @@ def bench_prefill(ctx, hip, config, steps, warmup, eager):
     plan = ctx.plan(q, key, value, cfg, kind)
     seconds = timed(ctx, hip, enqueue, steps, warmup, eager)
     got = ctx.download(out)
-    name, _, kernels = kernel_profile(ctx, enqueue, 10 if config != 5 else 3, f"c{config}")
+    name, _, kernels = kernel_profile(ctx, enqueue, 10 if config != 5 else 8, f"c{config}",
+                                      warm=2)
     q.free()
     out.free()
     cache.close()
     return c, dict(steps=steps, seconds=seconds, kernel=name, kernels=kernels, launches=1,
                    flops=c.flops(), plan=plan, out=got)
+
+
+def bench_dispatch_modes(ctx, hip, config: int, calls: int) -> dict:
+    """One prefill config timed four ways in one process, in this order and
+    twice over: a HIP graph replay of `calls` calls (the timed region's
+    method), one eager batch of `calls` calls between two stream events,
+    the per-dispatch events of an eager batch (every dispatch's duration),
+    and `calls` isolated eager calls, each after a device synchronize."""
+    c = workloads.case(config)
+    cache = ctx.kv_cache(1, c.kv_heads, c.head_dim, c.kv_length)
+    key, value = cache.layer(0)
+    ctx.upload(key, c.k)
+    ctx.upload(value, c.v)
+    q = ctx.tensor(c.q)
+    out = ctx.empty(c.q.shape)
+    cfg = mi_attn.AttentionConfig(c.q_heads, c.kv_heads, c.head_dim, True, c.query_offset)
+
+    def enqueue(batch, i):
+        return batch.attention(q, key, value, cfg, mi_attn.FLASH_PREFILL, out=out)
+
+    reps = []
+    for _ in range(2):
+        graph = timed(ctx, hip, enqueue, calls, 1, False)
+        eager = timed(ctx, hip, enqueue, calls, 1, True)
+        ctx.take_kernel_profiles()
+        ctx.set_kernel_profiling(True)
+        try:
+            batch = ctx.begin_batch()
+            keep = [enqueue(batch, i) for i in range(calls)]
+            batch.finish()
+            del keep
+            each = [ns / 1e3 for _, ns in ctx.take_kernel_profiles()]
+        finally:
+            ctx.set_kernel_profiling(False)
+        isolated = []
+        for _ in range(calls):
+            hip.check(hip.lib.hipDeviceSynchronize(), "sync")
+            isolated.append(time_eager(ctx, hip, enqueue, 1) * 1e6)
+        reps.append({"graph_us": round(graph * 1e6, 1), "eager_batch_us": round(eager * 1e6, 1),
+                     "dispatch_events_us": [round(x, 1) for x in each],
+                     "isolated_us": [round(x, 1) for x in isolated]})
+        log(f"dispatch modes c{config}: {reps[-1]}")
+    q.free()
+    out.free()
+    cache.close()
+    return {"workload": f"c{config}", "calls": calls, "runs": reps}
 
 
 # ---------------------------------------------------------------- o_proj --
@@ -565,7 +620,7 @@ def bench_floors(ctx, hip, steps) -> dict:
        on the attention kernel's grid (16 splits x 8 KV heads, 512 threads);
        the same grid loading exactly the attention kernel's K/V rows (the
        data phase); the data phase plus the split exchange (partials with
-       device-scope stores, release arrival, last-arriver acquire and merge,
+       device-scope stores, the arrival, the last arriver's acquire and merge,
        f16 output); and the attention call itself;
      - c4: a streaming read of c4's algorithmic bytes by 512 to 2048
        workgroups (the achievable HBM read rate at that size), beside the
@@ -854,7 +909,9 @@ def main() -> int:
                     help="comma list of c4 (headline), c5, c3, c2, c1, step (decode step "
                          "graphs), o_proj (with the other neighbours), compare (the "
                          "attention compare harness), floors (calibration kernels beside "
-                         "the decodes); profiling runs select one at a time")
+                         "the decodes), dispatch (c5 and c3 as graph replays, eager batches, "
+                         "per-dispatch events and isolated calls); profiling runs select "
+                         "one at a time")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of HIP graph replays (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -884,7 +941,8 @@ def main() -> int:
         print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
-    unknown = set(chosen) - {"c1", "c2", "c3", "c4", "c5", "step", "o_proj", "compare", "floors"}
+    unknown = set(chosen) - {"c1", "c2", "c3", "c4", "c5", "step", "o_proj", "compare", "floors",
+                             "dispatch"}
     if unknown:
         print(f"unknown workloads {sorted(unknown)}", file=sys.stderr)
         return 2
@@ -969,6 +1027,9 @@ def main() -> int:
         result["neighbours"] = bench_neighbours(ctx, hip, args.eager)
     if "floors" in chosen and not args.eager:
         result["floors"] = bench_floors(ctx, hip, 64)
+    if "dispatch" in chosen and not args.eager:
+        result["dispatch_modes"] = [bench_dispatch_modes(ctx, hip, 5, 4),
+                                    bench_dispatch_modes(ctx, hip, 3, 20)]
     if "compare" in chosen:
         result["compare"] = []
         for tokens, length in COMPARE_SHAPES:

@@ -74,3 +74,44 @@ def test_probe_split_exchange_leaves_counters_zero(ctx):
             assert got[h, s] == want, (h, s)
     for t in (k, v, partial, counters, words, out16):
         t.free()
+
+
+def test_dispatch_modes_report_every_mode(ctx):
+    """The dispatch-mode comparison times one prefill config as a graph
+    replay, an eager batch, per-dispatch events and isolated eager calls;
+    every mode yields one positive duration per call."""
+    report = bench.bench_dispatch_modes(ctx, bench.Hip(), 1, 3)
+    assert report["workload"] == "c1" and report["calls"] == 3 and len(report["runs"]) == 2
+    for run in report["runs"]:
+        assert run["graph_us"] > 0 and run["eager_batch_us"] > 0
+        assert len(run["dispatch_events_us"]) == 3 and min(run["dispatch_events_us"]) > 0
+        assert len(run["isolated_us"]) == 3 and min(run["isolated_us"]) > 0
+
+
+def test_kernel_profile_warm_calls_are_not_profiled(ctx):
+    """kernel_profile's warm-up calls run before profiling starts: only the
+    `count` calls' dispatches are reported."""
+    c = bench.workloads.case(1)
+    cache = ctx.kv_cache(1, c.kv_heads, c.head_dim, c.kv_length)
+    key, value = cache.layer(0)
+    ctx.upload(key, c.k)
+    ctx.upload(value, c.v)
+    q, out = ctx.tensor(c.q), ctx.empty(c.q.shape)
+    cfg = mi_attn.AttentionConfig(c.q_heads, c.kv_heads, c.head_dim, True, c.query_offset)
+    calls = []
+
+    def enqueue(batch, i):
+        calls.append(i)
+        return batch.attention(q, key, value, cfg, mi_attn.FLASH_PREFILL, out=out)
+
+    saved = bench.DISPATCH_EVENTS
+    bench.DISPATCH_EVENTS = True
+    try:
+        name, median, kernels = bench.kernel_profile(ctx, enqueue, 4, "c1", warm=2)
+    finally:
+        bench.DISPATCH_EVENTS = saved
+    assert len(calls) == 6 and name == "attn_prefill" and median > 0
+    assert set(kernels) == {"attn_prefill"}
+    q.free()
+    out.free()
+    cache.close()
