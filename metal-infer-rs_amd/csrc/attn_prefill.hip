@@ -14,7 +14,8 @@
 //    keys permuted (bits 2 and 3 of the key index swapped) to match the order
 //    in which the S^T accumulator holds them;
 //  - the next tile's K/V global loads are in flight while the current tile
-//    is computed; causally heavy row tiles are dispatched first.
+//    is computed; causally heavy row tiles are dispatched first (split plans:
+//    longest piece first, each CU's long piece paired with a short one).
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -73,8 +74,10 @@ constexpr int kReadAhead = 4;
 // waves sharing each K/V tile, one workgroup per CU). D = 256 runs one
 // 4-wave workgroup per CU: its Q operand and O accumulators (64 + 128
 // registers per lane) leave room for one wave per SIMD, and its two LDS
-// stages take 141 KB.
-template <int D, int BMT>
+// stages take 141 KB. ORDERED: a split plan whose pieces run in the host's
+// order (PrefillParams::order); a separate instantiation, so that the other
+// launches do not wait on the order entry's load.
+template <int D, int BMT, bool ORDERED>
 __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void attn_prefill_kernel(
     const PrefillParams p) {
   constexpr int BM = BMT;
@@ -117,9 +120,10 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   // Dispatch order: workgroups are handed out in linear-id order, and
   // round-robin over the 8 XCDs, so id % 8 selects the XCD. When the KV
   // heads split evenly over the XCDs, each XCD gets whole heads (their K/V
-  // stay in its L2). Within a head, row tiles go heaviest first and the
-  // gridDim.z key splits of one row tile go together; a split past the row
-  // tile's last key tile returns at once.
+  // stay in its L2). Within a head, an ordered split plan runs its pieces in
+  // the host's order (p.order); otherwise row tiles go heaviest first and
+  // the gridDim.z key splits of one row tile go together, a split past the
+  // row tile's last key tile returning at once.
   uint32_t tile, kvh, split;
   {
     const uint32_t id = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
@@ -133,8 +137,14 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       kvh = id % H;
       rest = id / H;
     }
-    tile = p.row_tiles - 1 - rest / S;
-    split = rest % S;
+    if constexpr (ORDERED) {
+      const uint32_t piece = p.order[rest];
+      tile = piece >> 4;
+      split = piece & 15;
+    } else {
+      tile = p.row_tiles - 1 - rest / S;
+      split = rest % S;
+    }
   }
   const uint32_t row0 = tile * BM;
   const uint32_t my_row = row0 + wave * 32 + n;
@@ -147,12 +157,23 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   const uint32_t kmax =
       p.causal != 0 ? (uint32_t)min(L, off + t_last + 1) : (uint32_t)L;
   const uint32_t n_tiles = (kmax + BN - 1) / BN;
-  // This split's key tiles [t_begin, t_end) and the row tile's split count.
+  // This split's key tiles [t_begin, t_end), and whether the row tile has
+  // other splits.
   const uint32_t per_split = p.split_tiles != 0 ? p.split_tiles : n_tiles;
-  const uint32_t t_begin = split * per_split;
-  if (t_begin >= n_tiles) return;  // the row tile needs fewer splits
-  const uint32_t t_end = min(n_tiles, t_begin + per_split);
-  const bool partial_out = n_tiles > per_split;
+  uint32_t t_begin, t_end;
+  bool partial_out;
+  if constexpr (ORDERED) {
+    const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
+    if (split >= nsplit) return;  // not in a plan the host made
+    t_begin = split * n_tiles / nsplit;
+    t_end = (split + 1) * n_tiles / nsplit;
+    partial_out = nsplit > 1;
+  } else {
+    t_begin = split * per_split;
+    if (t_begin >= n_tiles) return;  // the row tile needs fewer splits
+    t_end = min(n_tiles, t_begin + per_split);
+    partial_out = n_tiles > per_split;
+  }
   // Last visible key of this lane's row, and of the tile's first row (below
   // which no key needs a mask).
   const uint64_t lim =
@@ -509,6 +530,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __shared__ uint32_t s_last;
     __syncthreads();
+    // Both plans cut a row tile into ceil(n_tiles / split_tiles) splits.
     const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
     if (tid == 0) {
       uint32_t *counter = p.counters + tile * p.kv_heads + kvh;
@@ -612,20 +634,28 @@ bool prefill_supported(uint32_t head_dim) {
 }
 
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
-  // One workgroup per (row tile, KV head, key split).
-  const dim3 grid(p.row_tiles, p.kv_heads, p.splits > 1 ? p.splits : 1);
+  // One workgroup per piece of an ordered split plan, else per (row tile, KV
+  // head, key split).
+  const dim3 grid = p.pieces_per_head != 0
+                        ? dim3(p.pieces_per_head, p.kv_heads, 1)
+                        : dim3(p.row_tiles, p.kv_heads, p.splits > 1 ? p.splits : 1);
+  const bool ordered = p.pieces_per_head != 0;
+  if (ordered && (p.pieces_per_head > kPrefillOrderMax || p.block_m != 128 || head_dim > 128))
+    return hipErrorInvalidValue;
   switch (head_dim) {
     case 64:
       if (p.block_m != 128) return hipErrorInvalidValue;
-      return dispatch(attn_prefill_kernel<64, 128>, grid, dim3(256), 0, l, p);
+      return ordered ? dispatch(attn_prefill_kernel<64, 128, true>, grid, dim3(256), 0, l, p)
+                     : dispatch(attn_prefill_kernel<64, 128, false>, grid, dim3(256), 0, l, p);
     case 128:
       if (p.block_m == 256)
-        return dispatch(attn_prefill_kernel<128, 256>, grid, dim3(512), 0, l, p);
+        return dispatch(attn_prefill_kernel<128, 256, false>, grid, dim3(512), 0, l, p);
       if (p.block_m != 128) return hipErrorInvalidValue;
-      return dispatch(attn_prefill_kernel<128, 128>, grid, dim3(256), 0, l, p);
+      return ordered ? dispatch(attn_prefill_kernel<128, 128, true>, grid, dim3(256), 0, l, p)
+                     : dispatch(attn_prefill_kernel<128, 128, false>, grid, dim3(256), 0, l, p);
     case 256:
       if (p.block_m != 128) return hipErrorInvalidValue;
-      return dispatch(attn_prefill_kernel<256, 128>, grid, dim3(256), 0, l, p);
+      return dispatch(attn_prefill_kernel<256, 128, false>, grid, dim3(256), 0, l, p);
     default: return hipErrorInvalidValue;
   }
 }

@@ -127,6 +127,10 @@ struct QkNormRopeParams {
 };
 
 // MFMA flash prefill (FlashPrefill at head_dim 64 / 128 / 256).
+// Split prefill plans with at most this many pieces per KV head launch them
+// in an order chosen on the host (PrefillParams::order).
+constexpr uint32_t kPrefillOrderMax = 64;
+
 struct PrefillParams {
   const uint16_t *q;
   int64_t q_tok, q_head;
@@ -140,10 +144,9 @@ struct PrefillParams {
   uint32_t row_tiles;       // ceil(T * group / block_m)
   uint32_t block_m;         // packed rows per workgroup: 128, or 256 at D = 128
   float scale_log2;
-  // Split-K over keys (small grids): split z of a row tile covers key tiles
-  // [z * split_tiles, (z + 1) * split_tiles); split_tiles = 0 means one split
-  // per row tile. Each split of a row tile that needs several writes its
-  // unnormalised rows (m, l, O[D]) as f32 to `partial`, laid out
+  // Split-K over keys (small grids). Each split of a row tile that needs
+  // several writes its unnormalised rows (m, l, O[D]) as f32 to `partial`,
+  // laid out
   // [splits][row_tiles][kv_heads][block_m / 32 waves][kPrefillPartialSlots(D)][64 lanes]
   // float2, then counts its arrival in counters[tile * kv_heads + kv_head];
   // the last split to arrive merges all of them in split order and resets
@@ -152,6 +155,15 @@ struct PrefillParams {
   uint32_t *counters;
   uint32_t split_tiles;
   uint32_t splits;
+  // pieces_per_head != 0: the grid is (pieces_per_head, kv_heads) and the
+  // workgroup at position `rest` of its KV head runs the piece
+  // order[rest] = row tile << 4 | split, where a row tile of n key tiles has
+  // s = ceil(n / split_tiles) splits and split z covers key tiles
+  // [z n / s, (z + 1) n / s). pieces_per_head = 0: the grid is (row_tiles,
+  // kv_heads, splits) and split z covers key tiles [z * split_tiles,
+  // (z + 1) * split_tiles), or all of them when split_tiles = 0.
+  uint32_t pieces_per_head;
+  uint16_t order[kPrefillOrderMax];
 };
 
 // Split pass (one workgroup per key block; writes the output directly when a
@@ -258,8 +270,9 @@ constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim
 bool prefill_supported(uint32_t head_dim);
 // 128-row prefill workgroups resident per CU: two, or one at head_dim 256.
 constexpr uint32_t prefill_workgroups_per_cu(uint32_t head_dim) { return head_dim == 256 ? 1 : 2; }
-// One launch, split merges included: grid (row_tiles, kv_heads, splits);
-// a key split past its row tile's last key tile returns at once.
+// One launch, split merges included: grid (pieces_per_head, kv_heads) for an
+// ordered split plan, else (row_tiles, kv_heads, splits), where a key split
+// past its row tile's last key tile returns at once.
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
 // Capacity of a context's split-K arrival counters (row tiles x KV heads of
 // a split prefill grid).

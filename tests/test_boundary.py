@@ -234,10 +234,10 @@ def test_flash_prefill_routes_to_mfma_kernel():
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
     assert p["grid"][:2] == (128, 8) and p["block_threads"] == 256
     # c3: 2048 x 2 = 4096 packed rows. It takes key splits, which keep the
-    # 128-row tile at two workgroups per CU: 32 row tiles per KV head.
+    # 128-row tile at two workgroups per CU (256 threads).
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
-    assert p["grid"][:2] == (32, 8) and p["block_threads"] == 256, p
+    assert p["splits"] > 1 and p["block_threads"] == 256, p
 
 
 def _pieces(T, G, L, off, per_split_keys, block_m=128):
@@ -252,11 +252,12 @@ def _pieces(T, G, L, off, per_split_keys, block_m=128):
 
 def test_small_prefill_grids_split_the_keys():
     # c3: 256 workgroups of 128 rows on 256 CUs. The split count is the largest
-    # whose non-empty pieces all fit at two workgroups per CU: 3 splits of 11
-    # key tiles, 504 non-empty pieces in a grid of 32 x 8 x 3.
+    # whose non-empty pieces all fit at two workgroups per CU: at most 3 splits
+    # of at most 11 key tiles, 63 pieces per KV head, launched as an ordered
+    # grid of exactly those pieces (63 x 8).
     q, k = tensor((2048, 16, 128)), tensor((2048, 8, 128))
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
-    assert p["grid"] == (32, 8, 3) and p["splits"] == 3 and p["block_keys"] == 11 * 64
+    assert p["grid"] == (63, 8, 1) and p["splits"] == 3 and p["block_keys"] == 11 * 64
     assert p["block_threads"] == 256
     # (m, l) + 128 O values per row as f32, for 128 rows (4 waves) per row tile
     assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 4) * 64 * 2 * 4
@@ -264,6 +265,12 @@ def test_small_prefill_grids_split_the_keys():
     assert pieces == 63 and pieces * 8 <= 2 * 256
     finer = -(-max_tiles // 4) * 64  # one more split would not fit
     assert _pieces(2048, 2, 2048, 0, finer)[0] * 8 > 2 * 256
+    # more pieces per KV head than the ordered grid holds (64): the
+    # (row tile, KV head, split) grid, splits past a row tile's window empty
+    q, k = tensor((333, 16, 128)), tensor((633, 1, 128))
+    p = plan(q, k, k, AttentionConfig(16, 1, 128, True, 300), FLASH_PREFILL)
+    assert p["splits"] > 1 and p["grid"] == (42, 1, p["splits"]), p
+    assert _pieces(333, 16, 633, 300, p["block_keys"])[0] > 64
     # c5 fills the chip on its own: no split, no scratch
     q, k = tensor((4096, 64, 128)), tensor((20480, 8, 128))
     p = plan(q, k, k, AttentionConfig(64, 8, 128, True, 16384), FLASH_PREFILL)
