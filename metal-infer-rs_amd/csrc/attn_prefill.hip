@@ -1,4 +1,5 @@
-// MFMA flash prefill for gfx950 (AttentionKind::FlashPrefill at D = 64, 128, 256).
+// MFMA flash prefill for gfx950 (AttentionKind::FlashPrefill at D = 32, 64, 128,
+// 256).
 //
 // Replaces attention_flash_prefill_f16 (transformer.metal:1667-1822) with a
 // CDNA4 design:
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   constexpr int CPR = D / 8;          // 16-byte chunks per tile row
   constexpr int RPB = 1024 / (2 * D); // tile rows per 1 KB block
   static_assert(BM == 128 || (BM == 256 && D == 128), "row tile");
-  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
   constexpr int DC = D / 16;          // 16-wide d chunks of Q K^T
   constexpr int DT = D / 32;          // 32-row d tiles of O^T
   constexpr int KS = D + 8;           // K tile row stride (halves)
@@ -100,7 +101,8 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   // D = 64, 128: K and V tiles arrive by direct global->LDS loads as rows
   // of 16-byte chunks, XOR-swizzled (k_swizzle, v_swizzle) so that the K
   // operand reads and the V^T transpose reads are free of bank conflicts.
-  // D = 256: register staging, K padded, V stored transposed.
+  // D = 32, 256: register staging, K padded, V stored transposed (at D = 32
+  // a K row is 64 bytes, two S MFMAs deep, and O^T one 32-row d tile).
   constexpr bool DIRECT = D == 64 || D == 128;
   constexpr int K_ELEMS = DIRECT ? BN * D : BN * KS;
   constexpr int V_ELEMS = DIRECT ? BN * D : D * VS;
@@ -630,7 +632,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
 }  // namespace
 
 bool prefill_supported(uint32_t head_dim) {
-  return head_dim == 64 || head_dim == 128 || head_dim == 256;
+  return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l) {
@@ -643,6 +645,10 @@ hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launc
   if (ordered && (p.pieces_per_head > kPrefillOrderMax || p.block_m != 128 || head_dim > 128))
     return hipErrorInvalidValue;
   switch (head_dim) {
+    case 32:
+      if (p.block_m != 128) return hipErrorInvalidValue;
+      return ordered ? dispatch(attn_prefill_kernel<32, 128, true>, grid, dim3(256), 0, l, p)
+                     : dispatch(attn_prefill_kernel<32, 128, false>, grid, dim3(256), 0, l, p);
     case 64:
       if (p.block_m != 128) return hipErrorInvalidValue;
       return ordered ? dispatch(attn_prefill_kernel<64, 128, true>, grid, dim3(256), 0, l, p)

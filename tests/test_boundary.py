@@ -219,8 +219,8 @@ def test_prefix_and_reshape():
 
 
 def test_flash_prefill_routes_to_mfma_kernel():
-    for d, expected in ((128, "attn_prefill"), (64, "attn_prefill"), (32, "attn_rows"),
-                        (256, "attn_prefill")):
+    for d, expected in ((128, "attn_prefill"), (64, "attn_prefill"), (32, "attn_prefill"),
+                        (16, "attn_rows"), (256, "attn_prefill")):
         q, k = tensor((2048, 16, d)), tensor((2048, 8, d))
         p = plan(q, k, k, AttentionConfig(16, 8, d, True, 0), FLASH_PREFILL)
         assert p["kernel"] == expected, d

@@ -128,7 +128,7 @@ def test_c5_chunked_prefill_seeded(ctx):
     print(f"c5 {len(rows)} rows x 64 heads max-abs {err:.2e}")
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1)])
 def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
     rng = np.random.default_rng(hq * 100 + hkv + d)
@@ -167,7 +167,7 @@ def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
     assert_parity(out[rows], ref, label=f"T={T} hq={hq}")
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("hq,hkv,T,off,causal", [
     (8, 8, 700, 37, True), (16, 8, 1000, 300, True), (64, 8, 520, 37, True),
     (16, 1, 333, 300, True), (8, 2, 1500, 0, True), (8, 8, 520, 0, False)])
@@ -216,7 +216,7 @@ def _moving_max_inputs(rng, T, L, hq, hkv, d, pattern):
     return as16(q), as16(k), as16(v)
 
 
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("hq,hkv,T,off,pattern", [
     (16, 8, 1000, 300, "rising"),    # key splits
     (64, 8, 520, 2000, "rising"),
