@@ -21,6 +21,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "timeline.hpp"
 
 namespace mi {
 namespace kernels {
@@ -29,6 +30,10 @@ namespace {
 using namespace mi::dev;
 
 constexpr int BN = kPrefillBlockN;  // keys per KV tile
+
+#ifdef MI_TIMELINE
+__device__ uint64_t prefill_timeline[kTimelineSlots * kTimelineFields];
+#endif
 
 // Column of key `key` (0..63 within a tile) in the transposed V tile: bits
 // 2 and 3 swapped, which is the key order of the P operand (see above).
@@ -119,6 +124,12 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
   const uint32_t G = p.group;
+#ifdef MI_TIMELINE
+  const TimelineRow tl = timeline_start(
+      prefill_timeline, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), tid == 0);
+#else
+  const TimelineRow tl;
+#endif
   // Dispatch order: workgroups are handed out in linear-id order, and
   // round-robin over the 8 XCDs, so id % 8 selects the XCD. When the KV
   // heads split evenly over the XCDs, each XCD gets whole heads (their K/V
@@ -164,18 +175,27 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   const uint32_t per_split = p.split_tiles != 0 ? p.split_tiles : n_tiles;
   uint32_t t_begin, t_end;
   bool partial_out;
+  tl.set(7, (uint64_t)tile | (uint64_t)split << 16);
   if constexpr (ORDERED) {
     const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
-    if (split >= nsplit) return;  // not in a plan the host made
+    if (split >= nsplit) {  // not in a plan the host made
+      tl.now(2);
+      return;
+    }
     t_begin = split * n_tiles / nsplit;
     t_end = (split + 1) * n_tiles / nsplit;
     partial_out = nsplit > 1;
   } else {
     t_begin = split * per_split;
-    if (t_begin >= n_tiles) return;  // the row tile needs fewer splits
+    if (t_begin >= n_tiles) {  // the row tile needs fewer splits
+      tl.now(2);
+      return;
+    }
     t_end = min(n_tiles, t_begin + per_split);
     partial_out = n_tiles > per_split;
   }
+  tl.set(7, (uint64_t)tile | (uint64_t)split << 16 | (uint64_t)t_begin << 20 |
+                (uint64_t)t_end << 40);
   // Last visible key of this lane's row, and of the tile's first row (below
   // which no key needs a mask).
   const uint64_t lim =
@@ -483,6 +503,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     if (t_begin + 1 < t_end) load_tile((t_begin + 1) * BN);
     __syncthreads();
   }
+  tl.now(3);
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   uint32_t it = t_begin;
@@ -506,6 +527,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
   if (it < t_end) step(it, std::true_type{}, S0{});
 
   const float l_total = l_run + __shfl_xor(l_run, 32, 64);
+  tl.now(4);
   if (partial_out) {
     // Publish this split's unnormalised rows with device-scope stores, wait
     // until they have completed, then count the arrival. The last split of
@@ -532,6 +554,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __shared__ uint32_t s_last;
     __syncthreads();
+    tl.now(5);
     // Both plans cut a row tile into ceil(n_tiles / split_tiles) splits.
     const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
     if (tid == 0) {
@@ -543,9 +566,14 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       s_last = last;
+      if (last) tl.add(7, 1ull << 63);
     }
     __syncthreads();
-    if (s_last == 0 || !row_ok) return;
+    tl.now(6);
+    if (s_last == 0 || !row_ok) {
+      tl.now(2);
+      return;
+    }
     // Log-sum-exp merge in split order (deterministic whichever split
     // arrives last); this split's own rows come from registers. Split 0
     // holds key 0, so M is finite; a split in which a row saw no key has
@@ -627,6 +655,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       v.y = pack_f16x2(o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
       *reinterpret_cast<uint2 *>(orow + 32 * dt + 8 * q + 4 * h) = v;
     }
+  tl.now(2);
 }
 
 }  // namespace
@@ -668,3 +697,12 @@ hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launc
 
 }  // namespace kernels
 }  // namespace mi
+
+#ifdef MI_TIMELINE
+extern "C" int32_t mi_timeline_read_prefill(void *dst, uint64_t bytes) {
+  const uint64_t cap = sizeof(uint64_t) * mi::dev::kTimelineSlots * mi::dev::kTimelineFields;
+  if (dst == nullptr || bytes > cap) return hipErrorInvalidValue;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(mi::kernels::prefill_timeline), bytes, 0,
+                             hipMemcpyDeviceToHost);
+}
+#endif

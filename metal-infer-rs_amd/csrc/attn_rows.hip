@@ -24,6 +24,7 @@
 
 #include "device_common.hpp"
 #include "kernels.hpp"
+#include "timeline.hpp"
 
 namespace mi {
 namespace kernels {
@@ -558,6 +559,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
 constexpr int kStreamWaves = 4;
 constexpr int kStreamTile = 32;
 
+#ifdef MI_TIMELINE
+__device__ uint64_t stream_timeline[kTimelineSlots * kTimelineFields];
+#endif
+
 typedef float sf4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 load16_stream(const uint16_t *ptr) {
@@ -593,6 +598,11 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
+#ifdef MI_TIMELINE
+  const TimelineRow tl = timeline_start(stream_timeline, blockIdx.x, tid == 0);
+#else
+  const TimelineRow tl;
+#endif
   const uint32_t upb = p.kv_heads * p.head_chunks;  // units per sequence
   const float c2 = p.scale_log2;
   // Visible keys of sequence b: its cached length (one query at the end).
@@ -635,7 +645,10 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
   const uint32_t w = blockIdx.x;
   uint64_t pos = (uint64_t)w * seg;
   const uint64_t end = min(pos + seg, total);
-  if (pos >= end) return;
+  if (pos >= end) {
+    tl.now(2);
+    return;
+  }
   // The sequence holding key `at`: the last b with s_pre[b] <= at (which
   // skips sequences without keys).
   auto find_seq = [&](uint64_t at) -> uint32_t {
@@ -675,6 +688,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
   // (measured on MI355X, c4: 104.6-104.7 against 104.8-104.9 us per call
   // re-reading them from global memory with 64-bit divisions, bit-identical).
   const bool narrow = total <= 0xffffffffull;
+  tl.now(3);
   while (pos < end) {
     const uint32_t len_b = s_len[b];
     const uint64_t rel = pos - s_pre[b];
@@ -818,6 +832,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
     // Merge the waves through LDS, then write the unit's output (a piece
     // that is the whole unit) or this piece's partial.
     __syncthreads();
+    const uint64_t tl_loop_end = tl.clock();
     float *s_o = reinterpret_cast<float *>(v_lds_a);  // [WAVES][GC][D]
     if (col < GC) {
       if (grp == 0) {
@@ -859,9 +874,12 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
     }
     // The next piece's loads overwrite both stages.
     __syncthreads();
+    tl.add(4, 1 | (uint64_t)ntiles << 16);
+    tl.add(5, tl.clock() - tl_loop_end);
     pos += k1 - k0;
     if (pos < end && pos >= s_pre[b + 1]) b = find_seq(pos);
   }
+  tl.now(2);
 }
 
 // Merges the pieces of the split units of attn_decode_stream_kernel, one
@@ -1054,3 +1072,12 @@ hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
 
 }  // namespace kernels
 }  // namespace mi
+
+#ifdef MI_TIMELINE
+extern "C" int32_t mi_timeline_read_stream(void *dst, uint64_t bytes) {
+  const uint64_t cap = sizeof(uint64_t) * mi::dev::kTimelineSlots * mi::dev::kTimelineFields;
+  if (dst == nullptr || bytes > cap) return hipErrorInvalidValue;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(mi::kernels::stream_timeline), bytes, 0,
+                             hipMemcpyDeviceToHost);
+}
+#endif

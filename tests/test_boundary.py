@@ -320,6 +320,19 @@ def test_probe_library_exports_its_header():
     assert not set(names) & exported(ROOT / "metal-infer-rs_amd" / "libmi_attn.so")
 
 
+def test_timeline_library_is_the_attention_library_plus_its_readers():
+    """libmi_attn_timeline.so (include/mi_timeline.h) is built from the same
+    sources with per-workgroup timestamps: it exports every attention entry
+    point and the two readers; the product library exports no reader."""
+    pkg = ROOT / "metal-infer-rs_amd"
+    names = declared("mi_timeline.h")
+    assert sorted(names) == ["mi_timeline_read_prefill", "mi_timeline_read_stream"]
+    timeline = exported(pkg / "libmi_attn_timeline.so")
+    assert set(names) <= timeline
+    assert set(declared("mi_attn.h")) <= timeline
+    assert not set(names) & exported(pkg / "libmi_attn.so")
+
+
 def test_compare_statistics_follow_the_reference_indexing():
     """bench.rs:1995-2008: median = sorted[n / 2], p95 = sorted[round((n - 1)
     * 0.95)], mean over all samples, in ms."""
