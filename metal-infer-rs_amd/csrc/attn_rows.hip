@@ -542,9 +542,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
 //    of another; each such piece ends in one partial, at slot
 //    (workgroup + unit) (unique, and a unit's pieces are consecutive slots).
 //    attn_stream_merge_kernel, launched next on the same stream, merges the
-//    pieces of every split unit (stream order makes the partials visible;
-//    an in-launch merge would need a release per piece, which on MI355X
-//    writes back the XCD's L2 and measured 27% slower at 32 sequences).
+//    pieces of every split unit (stream order makes the partials visible).
+//    In-launch merges measured slower on MI355X at 32 sequences: 27% with a
+//    release per piece (an L2 writeback while the other workgroups stream),
+//    3% with every workgroup's arrivals counted at its segment's end (the
+//    last arrivers are the slow second workgroups of their CUs).
 //  - Per 32-key tile and wave: S^T[key][head] = K Q^T on
 //    v_mfma_f32_16x16x32_f16, K rows loaded straight into the A operand
 //    (lane (g, c) holds key c, d 8 g + 32 j) and Q^T as the B operand (head
