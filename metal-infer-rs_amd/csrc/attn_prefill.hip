@@ -58,6 +58,15 @@ __device__ __forceinline__ int v_swizzle(int r) {
   return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
 }
 
+// Output staging (the rows of one wave as f16 in LDS): 16-byte chunk c of
+// row r sits at chunk c ^ out_swizzle(r), so that the writes (one chunk of
+// 32 rows per instruction) and the reads (whole rows) spread over the banks.
+template <int D>
+__device__ __forceinline__ int out_swizzle(int r) {
+  constexpr int CPR = D / 8, RB = D >= 128 ? 1 : 128 / D;  // rows per 256 bytes
+  return (r / RB) & (CPR - 1);
+}
+
 __device__ __forceinline__ uint4 load16(const uint16_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
@@ -570,7 +579,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     }
     __syncthreads();
     tl.now(6);
-    if (s_last == 0 || !row_ok) {
+    if (s_last == 0) {
       tl.now(2);
       return;
     }
@@ -638,14 +647,21 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[dt][r] = acc[dt][r];
     l_run = lsum;  // the normalisation below divides by the merged sum
-  } else if (!row_ok) {
-    return;
   }
 
-  // Normalise and store: lane (h, n) holds d = 32dt + 8q + 4h + 0..3.
+  // Normalise, then store through LDS: lane (h, n) holds d = 32dt + 8q +
+  // 4h + 0..3 of row n, so stored directly every instruction would write
+  // 8-byte pieces of 32 rows. Each wave instead writes its 32 rows as f16
+  // into a region of the (now idle) K/V stages, chunks XOR-swizzled per row
+  // (out_swizzle), and stores them back as whole 16-byte chunks, D / 8
+  // consecutive lanes per row. Rows past the last token are not stored.
   const float inv = 1.0f / (partial_out ? l_run : l_total);
-  uint16_t *orow =
-      p.out + (int64_t)my_t * p.o_tok + (int64_t)(kvh * G + my_g) * p.o_head;
+  constexpr int CPR_OUT = D / 8;           // 16-byte chunks per output row
+  constexpr int RPI = 64 / CPR_OUT;        // rows per store instruction
+  static_assert(2 * 32 * D <= K_ELEMS && 2 * 32 * D <= V_ELEMS, "output staging");
+  __syncthreads();  // every wave is past its last LDS operand read
+  uint16_t *rows_lds =
+      (wave < 2 ? k_lds_a : wave < 4 ? k_lds_b : wave < 6 ? v_lds_a : v_lds_b) + (wave & 1) * 32 * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -653,8 +669,27 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
       uint2 v;
       v.x = pack_f16x2(o[dt][4 * q] * inv, o[dt][4 * q + 1] * inv);
       v.y = pack_f16x2(o[dt][4 * q + 2] * inv, o[dt][4 * q + 3] * inv);
-      *reinterpret_cast<uint2 *>(orow + 32 * dt + 8 * q + 4 * h) = v;
+      const int chunk = (4 * dt + q) ^ out_swizzle<D>(n);
+      *reinterpret_cast<uint2 *>(rows_lds + n * D + chunk * 8 + 4 * h) = v;
     }
+  __syncthreads();
+  // The lane index and the wave's first packed row are derived afresh (lane
+  // from mbcnt, the row from scalars) rather than taken from the prologue,
+  // whose values the compiler would otherwise keep, or spill, across the loop.
+  const int lane_o = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int c_out = lane_o % CPR_OUT;
+  const uint32_t wave_row0 = row0 + (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 32;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + lane_o / CPR_OUT;
+    const uint4 v = *reinterpret_cast<const uint4 *>(rows_lds + r * D +
+                                                     (c_out ^ out_swizzle<D>(r)) * 8);
+    const uint32_t prow = wave_row0 + r;
+    const uint32_t t = prow / G, g = prow % G;
+    if (t < p.tokens)
+      *reinterpret_cast<uint4 *>(p.out + (int64_t)t * p.o_tok + (int64_t)(kvh * G + g) * p.o_head +
+                                 c_out * 8) = v;
+  }
   tl.now(2);
 }
 

@@ -272,7 +272,8 @@ bool prefill_supported(uint32_t head_dim);
 constexpr uint32_t prefill_workgroups_per_cu(uint32_t head_dim) { return head_dim == 256 ? 1 : 2; }
 // One launch, split merges included: grid (pieces_per_head, kv_heads) for an
 // ordered split plan, else (row_tiles, kv_heads, splits), where a key split
-// past its row tile's last key tile returns at once.
+// past its row tile's last key tile returns at once. Q, K, V and the output
+// rows are 16-byte aligned (base and outer strides multiples of 8 elements).
 hipError_t launch_prefill(const PrefillParams &p, uint32_t head_dim, const Launch &l);
 // Capacity of a context's split-K arrival counters (row tiles x KV heads of
 // a split prefill grid).

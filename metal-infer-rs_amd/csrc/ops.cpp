@@ -310,7 +310,7 @@ mi_status plan_attention(const Context *ctx, const mi_tensor *q, const mi_tensor
   }
   if (kind == MI_ATTN_FLASH_PREFILL && kernels::prefill_supported(p.D) &&
       vector_friendly(*q, 8) && vector_friendly(*k, 8) && vector_friendly(*v, 8) &&
-      (out == nullptr || vector_friendly(*out, 4)) && (uint64_t)p.T * p.G < (1ull << 31) &&
+      (out == nullptr || vector_friendly(*out, 8)) && (uint64_t)p.T * p.G < (1ull << 31) &&
       // A key tile's per-lane byte offsets (64 rows from the tile base) are
       // unsigned 32-bit: both position strides non-negative, and 64 rows
       // span less than 4 GiB. Other views take the rows kernel (int64).

@@ -168,6 +168,46 @@ def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
+@pytest.mark.parametrize("offset,pad,kernel", [(8, 8, "attn_prefill"), (4, 4, "attn_rows")])
+def test_flash_prefill_strided_output(ctx, d, offset, pad, kernel):
+    """FlashPrefill into a strided view of a larger buffer (rows padded by
+    `pad` elements, the view starting `offset` elements in). Rows that are
+    16-byte aligned take the MFMA kernel, whose output leaves LDS as 16-byte
+    chunks of whole rows; 8-byte-aligned rows take the rows kernel. Both match
+    the oracle, and every element outside the view (padding, the ragged last
+    row tile's rows past the last token) keeps its sentinel."""
+    rng = np.random.default_rng(d + offset)
+    T, hq, hkv = 203, 8, 2  # 812 packed rows: the last 128-row tile is ragged
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((T, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((T, hkv, d)).astype(np.float16).view(np.uint16)
+    row = d + pad
+    sentinel = np.uint16(0x7BFF)  # f16 65504: no attention output reaches it
+    host = np.full(offset + T * hq * row + 64, sentinel, dtype=np.uint16)
+    buf = ctx.tensor(host)
+    out = buf.view((T, hq, d), (hq * row, row, 1), offset)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    ctx.take_kernel_profiles()
+    ctx.set_kernel_profiling(True)
+    try:
+        batch = ctx.begin_batch()
+        batch.attention(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v), cfg, mi_attn.FLASH_PREFILL,
+                        out=out)
+        batch.finish()
+        names = [name for name, _ in ctx.take_kernel_profiles()]
+    finally:
+        ctx.set_kernel_profiling(False)
+    assert kernel in names, names
+    got = ctx.download(buf)
+    inside = np.zeros(host.shape, dtype=bool)
+    idx = offset + (np.arange(T * hq)[:, None] * row + np.arange(d)[None, :])
+    inside[idx.ravel()] = True
+    assert (got[~inside] == sentinel).all(), "a store left the output view"
+    ref = oracle_attention(q, k, v, causal=True, hq=hq, hkv=hkv, d=d, off=0)
+    assert_parity(got[idx].reshape(T, hq, d), ref, label=f"d={d} offset={offset} pad={pad}")
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("hq,hkv,T,off,causal", [
     (8, 8, 700, 37, True), (16, 8, 1000, 300, True), (64, 8, 520, 37, True),
     (16, 1, 333, 300, True), (8, 2, 1500, 0, True), (8, 8, 520, 0, False)])
