@@ -128,6 +128,15 @@ def test_c5_chunked_prefill_seeded(ctx):
     print(f"c5 {len(rows)} rows x 64 heads max-abs {err:.2e}")
 
 
+def test_c5_chunked_prefill_full_output(ctx):
+    """Every one of c5's 4096 x 64 output rows against the oracle (the f32
+    restatement over all 16384 + 4096 keys; several seconds of host time on
+    the oracle's threads)."""
+    c = workloads.case(5)
+    err = _prefill_parity(ctx, c, "flash-prefill")
+    print(f"c5 all {c.tokens} tokens x 64 heads max-abs {err:.2e}")
+
+
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1)])
 def test_flash_prefill_gqa_ratios_and_offsets(ctx, d, hq, hkv):
