@@ -248,7 +248,10 @@ mi_status mi_context_take_kernel_profiles(mi_context *ctx,
  * stride; head-major cache prefixes are read in place), out [T, Hq, D] f16
  * caller-provided. Validation and error text follow ops.rs:1065-1150, with
  * one deliberate extension: FlashDecode accepts every GQA ratio (the
- * reference kernel is hard-wired to Hq == 2 * Hkv, ops.rs:1141-1145). */
+ * reference kernel is hard-wired to Hq == 2 * Hkv, ops.rs:1141-1145).
+ * FlashPrefill runs its MFMA kernel when q, k, v and out have 16-byte
+ * aligned rows (base and outer strides multiples of 8 elements); other
+ * views take the rows kernel, with the same results. */
 mi_status mi_attention(mi_batch *batch, const mi_tensor *q, const mi_tensor *k,
                        const mi_tensor *v, const mi_attention_config *config,
                        int32_t kind, const mi_tensor *out);
@@ -264,7 +267,8 @@ mi_status mi_attention_flash_decode_with_configuration(
     const mi_attention_config *config, uint32_t block_keys, uint32_t threads,
     const mi_tensor *out);
 /* Host-only dry run of mi_attention's validation and kernel choice
- * (ops.rs:1065-1150). block_keys/threads = 0 picks the defaults. */
+ * (ops.rs:1065-1150). block_keys/threads = 0 picks the defaults. The
+ * choice assumes an output with 16-byte aligned rows. */
 mi_status mi_attention_plan(const mi_context *ctx, const mi_tensor *q,
                             const mi_tensor *k, const mi_tensor *v,
                             const mi_attention_config *config, int32_t kind,
