@@ -381,13 +381,17 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     // Online softmax of row n over this lane's 32 keys (MASK: causal and
     // length mask, needed only past the first row's window).
     if constexpr (MASK) {
+      // Key 32 mt + 8 (r >> 2) + 4 h + (r & 3) of the tile is visible when
+      // it is at most lim_rel. The lane's 4 h moves to the limit, so each
+      // compare is against a constant (no per-key lane values to keep).
       const int lim_rel = (int)max(min((int64_t)lim - (int64_t)j0, (int64_t)BN), (int64_t)-1);
+      const int lim_lane = lim_rel - 4 * h;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key_rel = 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
-          s[mt][r] = key_rel > lim_rel ? -INFINITY : s[mt][r];
+          const int key_c = 32 * mt + 8 * (r >> 2) + (r & 3);
+          s[mt][r] = key_c > lim_lane ? -INFINITY : s[mt][r];
         }
     }
     // P = 2^(s c2 - m_ref c2) against the row's reference max m_run, as f16
