@@ -4,7 +4,7 @@
  * libmi_attn.so compiled with MI_TIMELINE).
  *
  * Not part of the attention ABI and with no counterpart in the reference:
- * a measurement aid. It exports everything libmi_attn.so does, plus the two
+ * a measurement aid. It exports everything libmi_attn.so does, plus the
  * readers below. Each kernel launch overwrites the rows of the workgroups it
  * runs; a row is kTimelineFields = 8 u64 words, row i for the workgroup of
  * linear id i (at most 8192 rows). Times are s_memrealtime ticks (100 MHz,
@@ -21,8 +21,17 @@
  *   7 row tile | split << 16 | first key tile << 20 | end key tile << 40 |
  *   (1 << 63 if it merged the row tile's splits).
  *
- * Both readers copy `bytes` from the start of the kernel's row buffer to the
- * host buffer `dst` (synchronous) and return the hipError_t (0 on success).
+ * Rows kernel (attn_rows_kernel: single-sequence decode and the other
+ * split-K kinds):
+ *   2 end time; 3 the first batch of K/V rows (and the query rows) loaded
+ *   (this build waits for them there, before the arithmetic); 4 key loop
+ *   done; 5 split partial stored and complete (0 if none); 6 arrival counted
+ *   (0 if none); 7 split | splits << 16 | (1 << 63 if it merged the unit's
+ *   splits).
+ *
+ * Every reader copies `bytes` from the start of its kernel's row buffer to
+ * the host buffer `dst` (synchronous) and returns the hipError_t (0 on
+ * success).
  */
 #ifndef MI_TIMELINE_H
 #define MI_TIMELINE_H
@@ -33,6 +42,7 @@
 extern "C" {
 #endif
 
+int32_t mi_timeline_read_rows(void *dst, uint64_t bytes);
 int32_t mi_timeline_read_stream(void *dst, uint64_t bytes);
 int32_t mi_timeline_read_prefill(void *dst, uint64_t bytes);
 

@@ -206,6 +206,10 @@ __device__ __forceinline__ Vec<8> norm_rope_row(const Vec<8> &raw, const Vec<8> 
 // device-scope stores and counts its arrival in p.counters[unit]; the last
 // split to arrive merges all of them in split order (no second launch).
 // STEP: the decode step (RowsParams::step_k), D = 128 and one token only.
+#ifdef MI_TIMELINE
+__device__ uint64_t rows_timeline[kTimelineSlots * kTimelineFields];
+#endif
+
 template <int D, int WAVES, int GC, bool FUSED, bool STEP = false>
 __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     const RowsParams p) {
@@ -233,6 +237,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   const uint32_t b = blockIdx.z / p.tokens;
   const uint32_t t = blockIdx.z % p.tokens;
   const uint32_t unit = blockIdx.z * gridDim.y + blockIdx.y;
+#ifdef MI_TIMELINE
+  const TimelineRow tl = timeline_start(
+      rows_timeline, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), tid == 0);
+#else
+  const TimelineRow tl;
+#endif
 
   uint32_t len = p.kv_length;
   uint32_t off = p.query_offset;
@@ -256,7 +266,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         out[(idx / D) * p.o_head + idx % D] = 0x7e00;
     return;
   }
-  if (split >= nsplits) return;
+  if (split >= nsplits) {
+    tl.now(2);
+    return;
+  }
+  tl.set(7, (uint64_t)split | (uint64_t)nsplits << 16);
 
   const uint32_t k0 = split * p.block_keys;
   const uint32_t k1 = min(available, k0 + p.block_keys);
@@ -429,6 +443,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         }
     }
   };
+#ifdef MI_TIMELINE
+  // Timeline build only: wait for the first batch (and the query rows), so
+  // that word 3 marks the data's arrival apart from the arithmetic.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  tl.now(3);
+#endif
   while (key < k1) {
     uint32_t next = key + R * U;
     if (next < k1) load_batch(next, kb2, vb2);
@@ -443,6 +463,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     key = next;
   }
 
+  tl.now(4);
   // Merge the key rows of this wave (lanes that differ in their row bits).
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
@@ -510,11 +531,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     }
   }
   if constexpr (FUSED) {
-    if (direct) return;
+    if (direct) {
+      tl.now(2);
+      return;
+    }
     // Every store of this workgroup has completed before the arrival counts.
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __shared__ uint32_t s_last;
     __syncthreads();
+    tl.now(5);
     if (tid == 0) {
       const uint32_t arrived = arrive(p.counters + unit);
       const bool last = arrived == nsplits - 1;
@@ -523,11 +548,17 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       s_last = last;
+      if (last) tl.add(7, 1ull << 63);
     }
     __syncthreads();
-    if (s_last == 0) return;
+    tl.now(6);
+    if (s_last == 0) {
+      tl.now(2);
+      return;
+    }
     merge_splits<D, GC, THREADS, true>(p, unit, nsplits, out);
   }
+  tl.now(2);
 }
 
 
@@ -1076,6 +1107,12 @@ hipError_t launch_rows(const RowsParams &p, uint32_t head_dim, uint32_t waves,
 }  // namespace mi
 
 #ifdef MI_TIMELINE
+extern "C" int32_t mi_timeline_read_rows(void *dst, uint64_t bytes) {
+  const uint64_t cap = sizeof(uint64_t) * mi::dev::kTimelineSlots * mi::dev::kTimelineFields;
+  if (dst == nullptr || bytes > cap) return hipErrorInvalidValue;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(mi::kernels::rows_timeline), bytes, 0,
+                             hipMemcpyDeviceToHost);
+}
 extern "C" int32_t mi_timeline_read_stream(void *dst, uint64_t bytes) {
   const uint64_t cap = sizeof(uint64_t) * mi::dev::kTimelineSlots * mi::dev::kTimelineFields;
   if (dst == nullptr || bytes > cap) return hipErrorInvalidValue;

@@ -1,6 +1,7 @@
-"""Per-workgroup timelines of the c4 batched decode and the c3 prefill.
+"""Per-workgroup timelines of the c4 batched decode, the c3 prefill and the
+c2 single-sequence decode.
 
-    python3 metal-infer-rs_amd/timeline.py [--workloads c4,c3] [--replays 3]
+    python3 metal-infer-rs_amd/timeline.py [--workloads c4,c3,c2] [--replays 3]
         [--json PATH]
 
 Loads the timeline build of the library (libmi_attn_timeline.so: the same
@@ -15,7 +16,11 @@ summary per replay:
    number of workgroups still running in 5 us bins;
  - c3 (attn_prefill_kernel): the first K/V tile's arrival, the key loop's
    end, the split epilogue (publish, arrival, the last arriver's merge), the
-   per-key-tile time of the CUs' first and second slots, and the span.
+   per-key-tile time of the CUs' first and second slots, and the span;
+ - c2 (attn_rows_kernel, FlashDecode): the spread of the workgroups' starts,
+   the first K/V batch's arrival (this build waits for it before the
+   arithmetic), the arithmetic, the wave merge with the partial's stores and
+   their completion, the arrival, the last arriver's merge, and the span.
 
 A measurement aid, not part of the attention path; nothing else imports it.
 """
@@ -187,20 +192,65 @@ def c3_timeline(hip, ctx, lib, replays: int) -> list[dict]:
     return reports
 
 
+def c2_timeline(hip, ctx, lib, replays: int) -> list[dict]:
+    c = workloads.case(2)
+    cache = ctx.kv_cache(1, c.kv_heads, c.head_dim, c.kv_length)
+    key, value = cache.layer(0)
+    ctx.upload(key, c.k)
+    ctx.upload(value, c.v)
+    q, out = ctx.tensor(c.q), ctx.empty(c.q.shape)
+    cfg = mi_attn.AttentionConfig(c.q_heads, c.kv_heads, c.head_dim, True, c.query_offset)
+    plan = ctx.plan(q, key, value, cfg, mi_attn.FLASH_DECODE)
+    wgs = int(np.prod(plan["grid"]))
+
+    def enqueue(batch, i):
+        return batch.attention(q, key, value, cfg, mi_attn.FLASH_DECODE, out=out)
+
+    def med(x):
+        return round(float(np.median(x)), 2) if len(x) else None
+
+    reports = []
+    for seconds, rows in replay(hip, ctx, enqueue, replays,
+                                lambda: read_rows(lib.mi_timeline_read_rows, wgs)):
+        merged = (rows[:, 7] >> np.uint64(63)) == 1
+        rows = rows.astype(np.int64)
+        t0 = rows[:, 0].min()
+        us = lambda f: (rows[:, f] - t0) * TICK_US  # noqa: E731
+        start, end, ready, loop, pub, arr = us(0), us(2), us(3), us(4), us(5), us(6)
+        published = rows[:, 5] > 0
+        last = int(np.argmax(end))
+        reports.append({
+            "workload": "c2", "plan_grid": list(plan["grid"]), "splits": plan["splits"],
+            "graph_us": round(seconds * 1e6, 2), "span_us": round(float(end.max()), 2),
+            "start_spread_us": round(float(start.max()), 2),
+            "first_batch_ready_us_median": med(ready - start),
+            "arithmetic_us_median": med(loop - ready),
+            "wave_merge_and_publish_us_median": med((pub - loop)[published]),
+            "arrival_us_median": med((arr - pub)[published]),
+            "merge_us_median": med((end - arr)[published & merged]),
+            "last_workgroup_us": {k: round(float(v[last]), 2) for k, v in
+                                  (("start", start), ("ready", ready), ("loop_end", loop),
+                                   ("published", pub), ("arrived", arr), ("end", end))}})
+    q.free()
+    out.free()
+    cache.close()
+    return reports
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workloads", default="c4,c3")
+    ap.add_argument("--workloads", default="c4,c3,c2")
     ap.add_argument("--replays", type=int, default=3)
     ap.add_argument("--json", default="")
     args = ap.parse_args()
     chosen = [w.strip() for w in args.workloads.split(",") if w.strip()]
-    if set(chosen) - {"c4", "c3"} or args.replays < 1:
-        print("workloads: c4, c3; replays >= 1", file=sys.stderr)
+    if set(chosen) - {"c4", "c3", "c2"} or args.replays < 1:
+        print("workloads: c4, c3, c2; replays >= 1", file=sys.stderr)
         return 2
     hip = bench.Hip()
     ctx = mi_attn.Context(0)
     lib = mi_attn.lib()
-    for name in ("mi_timeline_read_stream", "mi_timeline_read_prefill"):
+    for name in ("mi_timeline_read_stream", "mi_timeline_read_prefill", "mi_timeline_read_rows"):
         getattr(lib, name).argtypes = [ctypes.c_void_p, ctypes.c_uint64]
         getattr(lib, name).restype = ctypes.c_int32
     result = {"device": ctx.device_name, "compute_units": ctx.compute_units, "replays": []}
@@ -208,6 +258,8 @@ def main() -> int:
         result["replays"] += c4_timeline(hip, ctx, lib, args.replays)
     if "c3" in chosen:
         result["replays"] += c3_timeline(hip, ctx, lib, args.replays)
+    if "c2" in chosen:
+        result["replays"] += c2_timeline(hip, ctx, lib, args.replays)
     for r in result["replays"]:
         print(json.dumps(r), flush=True)
     if args.json:

@@ -326,7 +326,8 @@ def test_timeline_library_is_the_attention_library_plus_its_readers():
     point and the two readers; the product library exports no reader."""
     pkg = ROOT / "metal-infer-rs_amd"
     names = declared("mi_timeline.h")
-    assert sorted(names) == ["mi_timeline_read_prefill", "mi_timeline_read_stream"]
+    assert sorted(names) == ["mi_timeline_read_prefill", "mi_timeline_read_rows",
+                             "mi_timeline_read_stream"]
     timeline = exported(pkg / "libmi_attn_timeline.so")
     assert set(names) <= timeline
     assert set(declared("mi_attn.h")) <= timeline

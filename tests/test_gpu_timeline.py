@@ -1,6 +1,6 @@
 """GPU check of the timeline build (libmi_attn_timeline.so,
-include/mi_timeline.h): metal-infer-rs_amd/timeline.py replays c4 and c3
-once in its own process and reports per-workgroup timelines whose stamps are
+include/mi_timeline.h): metal-infer-rs_amd/timeline.py replays c4, c3 and
+c2 once in its own process and reports per-workgroup timelines whose stamps are
 ordered and complete."""
 from __future__ import annotations
 
@@ -22,7 +22,7 @@ def test_timeline_reports_ordered_stamps(tmp_path):
                     "--replays", "1", "--json", str(out)], check=True, timeout=300)
     result = json.loads(out.read_text())
     by = {r["workload"]: r for r in result["replays"]}
-    c4, c3 = by["c4"], by["c3"]
+    c4, c3, c2 = by["c4"], by["c3"], by["c2"]
     # c4: every workgroup of the stream-K grid ran (two per CU) and ended
     # after its prologue; pieces are 1 to 3 per workgroup.
     assert 0 < c4["prologue_us_median"] < c4["span_us"] <= c4["graph_us"]
@@ -38,3 +38,11 @@ def test_timeline_reports_ordered_stamps(tmp_path):
     assert c3["publish_us_median"] > 0 and c3["arrival_us_median"] > 0
     assert c3["merge_us_median"] > 0
     assert c3["span_us"] <= c3["graph_us"]
+    # c2: the (split, KV head) grid of FlashDecode; every split but the
+    # merger's publishes, arrives, and the last arriver of each head merges.
+    assert c2["splits"] > 1 and c2["plan_grid"][1] == 8
+    last = c2["last_workgroup_us"]
+    assert (last["start"] <= last["ready"] <= last["loop_end"] <= last["published"]
+            <= last["arrived"] <= last["end"] == c2["span_us"])
+    assert c2["first_batch_ready_us_median"] > 0 and c2["merge_us_median"] > 0
+    assert c2["span_us"] <= c2["graph_us"]
