@@ -571,7 +571,7 @@ __global__ __launch_bounds__(BMT * 2, (BMT == 128 && D <= 128) ? 2 : 1) void att
     // Both plans cut a row tile into ceil(n_tiles / split_tiles) splits.
     const uint32_t nsplit = (n_tiles + per_split - 1) / per_split;
     if (tid == 0) {
-      uint32_t *counter = p.counters + tile * p.kv_heads + kvh;
+      uint32_t *counter = p.counters + (size_t)(tile * p.kv_heads + kvh) * p.counter_stride;
       const uint32_t arrived = arrive(counter);
       const bool last = arrived == nsplit - 1;
       if (last) {

@@ -203,7 +203,7 @@ __device__ __forceinline__ Vec<8> norm_rope_row(const Vec<8> &raw, const Vec<8> 
 }
 
 // FUSED: with more than one split, each split publishes its partial with
-// device-scope stores and counts its arrival in p.counters[unit]; the last
+// device-scope stores and counts its arrival on the unit's counter; the last
 // split to arrive merges all of them in split order (no second launch).
 // STEP: the decode step (RowsParams::step_k), D = 128 and one token only.
 #ifdef MI_TIMELINE
@@ -541,11 +541,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
     __syncthreads();
     tl.now(5);
     if (tid == 0) {
-      const uint32_t arrived = arrive(p.counters + unit);
+      uint32_t *counter = p.counters + (size_t)unit * p.counter_stride;
+      const uint32_t arrived = arrive(counter);
       const bool last = arrived == nsplits - 1;
       if (last) {
         acquire_partials();
-        __hip_atomic_store(p.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       s_last = last;
       if (last) tl.add(7, 1ull << 63);

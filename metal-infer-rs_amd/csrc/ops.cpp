@@ -375,6 +375,7 @@ mi_status run_rows(Batch *batch, const AttnPlan &p, kernels::RowsParams rp,
   const bool events = src.fixed == nullptr;
   rp.partial = static_cast<float *>(scratch);
   rp.counters = p.fused ? ctx->split_counters : nullptr;
+  rp.counter_stride = kernels::counter_stride(p.units, ctx->split_counter_count);
   rp.block_keys = p.block_keys;
   rp.max_splits = p.splits;
   rp.head_chunks = p.G / p.chunk;
@@ -457,6 +458,8 @@ mi_status run_attention(Batch *batch, const mi_tensor *q, const mi_tensor *k,
     }
     pp.partial = static_cast<float *>(scratch);
     pp.counters = batch->ctx->split_counters;
+    pp.counter_stride =
+        kernels::counter_stride((uint64_t)pp.row_tiles * p.Hkv, batch->ctx->split_counter_count);
     st = launch(batch, p.kernel, [&](const kernels::Launch &s) {
       return kernels::launch_prefill(pp, p.D, s);
     });

@@ -426,7 +426,7 @@ def test_batched_decode_gqa_ratios_and_ragged_lengths(ctx, hq, hkv, d):
     (1024, 8, 2, 24, [(b * 7) % 25 for b in range(1024)]),
     # GQA 16 over 512 sequences (2048 units of 16 heads).
     (512, 64, 4, 20, [1 + (b * 5) % 20 for b in range(512)]),
-    # 8192 units (more than the context's split-K arrival counters).
+    # 8192 units.
     (1024, 32, 8, 12, [1 + (b * 3) % 12 for b in range(1024)]),
 ])
 def test_batched_decode_stream_k(ctx, B, hq, hkv, cap, lengths):
@@ -532,8 +532,9 @@ def test_batched_decode_beyond_the_stream_batch_limit(ctx):
 
 def test_batched_decode_beyond_the_arrival_counters(ctx):
     """More (sequence, KV head) units than the context's arrival counters:
-    the split partials are merged by a second launch instead."""
-    B, hq, hkv, d, cap = 600, 8, 8, 64, 40
+    the split partials are merged by a second launch instead (16,800 units
+    against 16,384 counters)."""
+    B, hq, hkv, d, cap = 2100, 8, 8, 64, 40
     lengths = [40 - (b % 13) for b in range(B)]
     q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, 5, B, hq, hkv, d, cap, lengths)
     cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
