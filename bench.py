@@ -639,7 +639,7 @@ def bench_floors(ctx, hip, steps) -> dict:
         ctx.upload(value, c.v)
     head_stride = layers[0][0].strides[1]
     partial = ctx.empty((hkv * splits * group * (d + 2),), mi_attn.F32)
-    counters = ctx.tensor(np.zeros(hkv, np.uint32), mi_attn.U32)
+    counters = ctx.tensor(np.zeros(32 * hkv, np.uint32), mi_attn.U32)  # one line per head
     words = ctx.empty((hkv * splits,), mi_attn.U32)
     out16 = ctx.empty((hkv * group * d,))
     q = ctx.tensor(c.q)

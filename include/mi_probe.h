@@ -42,12 +42,13 @@ int32_t mi_probe_read(void *stream, const void *src, uint64_t bytes_per_workgrou
  *  - publish != 0: each workgroup stores a (max, sum, acc[128]) partial for
  *    each of the `group` query heads of its KV head into `partial` (unit x
  *    split x group x 130 floats) with device-scope stores, waits for them,
- *    counts its arrival on counters[kv head] with an agent-scope atomic add,
+ *    counts its arrival on counters[32 * kv head] with an agent-scope
+ *    atomic add (one 128-byte line per counter, as the attention kernels),
  *    and the last split to arrive acquires, resets the counter to zero and
  *    merges every split's partial (one load per split per output element)
  *    into out_f16 [group x 128 halves per KV head] — the attention kernel's
  *    split protocol.
- * `counters` holds kv_heads zeroed words (left zeroed). group <= 8. */
+ * `counters` holds 32 * kv_heads zeroed words (left zeroed). group <= 8. */
 int32_t mi_probe_split_decode(void *stream, const uint16_t *k, const uint16_t *v,
                               uint64_t head_stride, uint32_t kv_heads, uint32_t group,
                               uint32_t keys, uint32_t block_keys, int32_t publish,

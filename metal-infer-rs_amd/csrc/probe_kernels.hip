@@ -56,6 +56,10 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerRound = kWaves * 4;
 constexpr int kBatches = 4;
 constexpr int kMergeChunk = 16;
+// Words between two KV heads' arrival counters: one 128-byte line each, as
+// the attention kernels keep theirs (arrivals on one line queue behind each
+// other).
+constexpr uint32_t kProbeCounterStride = 32;
 
 struct SplitArgs {
   const uint16_t *k, *v;
@@ -114,10 +118,11 @@ __global__ __launch_bounds__(kThreads) void probe_split_decode_kernel(const Spli
     __shared__ uint32_t s_last;
     __syncthreads();
     if (tid == 0) {
-      const bool last = arrive(a.counters + unit) == splits - 1;
+      const bool last = arrive(a.counters + (size_t)unit * kProbeCounterStride) == splits - 1;
       if (last) {
         acquire_partials();
-        __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.counters + (size_t)unit * kProbeCounterStride, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
       s_last = last;
     }

@@ -47,7 +47,7 @@ def test_probe_split_exchange_leaves_counters_zero(ctx):
     k, v = ctx.tensor(store), ctx.tensor(store[:, ::-1].copy())
     splits = (L + block - 1) // block
     partial = ctx.empty((hkv * splits * group * (d + 2),), mi_attn.F32)
-    counters = ctx.tensor(np.zeros(hkv, np.uint32), mi_attn.U32)
+    counters = ctx.tensor(np.zeros(32 * hkv, np.uint32), mi_attn.U32)  # one line per head
     words = ctx.empty((hkv * splits,), mi_attn.U32)
     out16 = ctx.empty((hkv * group * d,))
     for publish in (0, 1, 1):
