@@ -530,6 +530,38 @@ def test_batched_decode_beyond_the_stream_batch_limit(ctx):
         assert_parity(got[b:b + 1], ref, label=f"seq {b}")
 
 
+@pytest.mark.parametrize("B", [1, 128, 600, 2048])
+def test_batched_decode_counter_spacing(ctx, B):
+    """The in-launch merge of the rows kernel at every arrival-counter
+    spacing: 8 units (one 128-byte line per counter), 1024 (16 words apart),
+    4800 (2 words) and 16,384 (the whole buffer, adjacent words). Sampled
+    sequences match the oracle, and a second call, which needs every counter
+    back at zero, is bit-identical."""
+    hq, hkv, d, cap = 8, 8, 64, 40
+    lengths = [40 - (b % 13) for b in range(B)]
+    q, k, v, kt, vt, kview, vview, lt = _batched_case(ctx, 11 + B, B, hq, hkv, d, cap, lengths)
+    qt = ctx.tensor(q)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    outs = []
+    for _ in range(2):
+        ctx.take_kernel_profiles()
+        ctx.set_kernel_profiling(True)
+        try:
+            batch = ctx.begin_batch()
+            out = batch.attention_decode_batched(qt, kview, vview, lt, cfg, 16)
+            batch.finish()
+            names = [name for name, _ in ctx.take_kernel_profiles()]
+        finally:
+            ctx.set_kernel_profiling(False)
+        assert names == ["attn_rows_batched"], names  # merged inside the launch
+        outs.append(ctx.download(out))
+    assert np.array_equal(outs[0], outs[1])
+    for b in sorted({0, B // 2, B - 1} | set(range(0, B, max(1, B // 16)))):
+        n = lengths[b]
+        ref = oracle_attention(q[b:b + 1], k[b, :n], v[b, :n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(outs[0][b:b + 1], ref, label=f"B={B} seq {b}")
+
+
 def test_batched_decode_beyond_the_arrival_counters(ctx):
     """More (sequence, KV head) units than the context's arrival counters:
     the split partials are merged by a second launch instead (16,800 units
