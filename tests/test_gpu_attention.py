@@ -177,6 +177,32 @@ def test_flash_prefill_256_row_tiles(ctx, hq, hkv, T, off, causal):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
+@pytest.mark.parametrize("T,off,L,causal", [
+    (300, 100, 477, True),   # 77 cached keys past the last row's window
+    (300, 100, 250, True),   # cache shorter than the window: late rows see all L keys
+    (300, 0, 70, False),     # fewer keys than query rows
+    (129, 0, 1, False),      # one key
+    (200, 5000, 5200, True)])  # long offset, split plan
+def test_flash_prefill_key_length_edges(ctx, d, T, off, L, causal):
+    """FlashPrefill where the key count is not offset + T: keys past every
+    row's causal window (they must have no influence), a cache shorter than
+    the causal window (the availability min(L, offset + t + 1) of
+    transformer.metal:1589-1590), fewer keys than rows, and a single key."""
+    hq, hkv = 16, 4
+    rng = np.random.default_rng(T + L + d)
+    q = rng.standard_normal((T, hq, d)).astype(np.float16).view(np.uint16)
+    k = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((L, hkv, d)).astype(np.float16).view(np.uint16)
+    geo = dict(hq=hq, hkv=hkv, d=d, off=off)
+    info = ctx.plan(ctx.tensor(q), ctx.tensor(k), ctx.tensor(v),
+                    mi_attn.AttentionConfig(hq, hkv, d, causal, off), mi_attn.FLASH_PREFILL)
+    assert info["kernel"] == "attn_prefill", info
+    out = run_attention(ctx, q, k, v, kind="flash-prefill", causal=causal, **geo)
+    ref = oracle_attention(q, k, v, causal=causal, **geo)
+    assert_parity(out, ref, label=f"T={T} off={off} L={L} causal={causal} plan={info}")
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("offset,pad,kernel", [(8, 8, "attn_prefill"), (4, 4, "attn_rows")])
 def test_flash_prefill_strided_output(ctx, d, offset, pad, kernel):
     """FlashPrefill into a strided view of a larger buffer (rows padded by
