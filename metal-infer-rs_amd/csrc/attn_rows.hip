@@ -880,7 +880,18 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
     }
     __syncthreads();
     const bool direct = first_wg == last_wg;
-    float *part = p.partial + (size_t)(w + unit) * GC * (D + 2);
+    // Slot of this piece (kernels.hpp, launch_decode_stream): the unit's own
+    // slots when it has few pieces, so that the merge launch can load them
+    // with its descriptor in one round trip, else the overflow slots.
+    const uint32_t units = p.batch * upb, pieces = last_wg - first_wg + 1;
+    const size_t slot = pieces <= kStreamUnitSlots
+                            ? (size_t)unit * kStreamUnitSlots + (w - first_wg)
+                            : (size_t)units * kStreamUnitSlots + w + unit;
+    float *part = p.partial + slot * GC * (D + 2);
+    if (w == first_wg && tid == 0)
+      reinterpret_cast<uint32_t *>(p.partial + (size_t)units * (kStreamUnitSlots + 1) * GC * (D + 2) +
+                                   (size_t)p.stream_workgroups * GC * (D + 2))[unit] =
+          first_wg | pieces << 16;
     for (int idx = tid; idx < GC * D; idx += THREADS) {
       const int g = idx / D, d = idx % D;
       float M = -INFINITY;
@@ -917,14 +928,18 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
 }
 
 // Merges the pieces of the split units of attn_decode_stream_kernel, one
-// workgroup per unit (256 threads), in piece order: the log-sum-exp combine
-// of the reference's reduce kernels (transformer.metal:2251-2316). Recomputes
-// the stream kernel's segmentation (the key prefix sums over all sequences,
-// the segment size for p.stream_workgroups workgroups) to find the unit's
-// pieces; units held by one workgroup were written directly. One thread per
-// output element (GC x 128, at least 256, at most 1024), so the partials are
-// loaded in one pass (measured on MI355X at c4, GQA 4: 105.7 against 106.0 us
-// per call with 256 threads and two passes, bit-identical).
+// workgroup per unit, in piece order: the log-sum-exp combine of the
+// reference's reduce kernels (transformer.metal:2251-2316). The unit's
+// descriptor (first workgroup, pieces), its length and its own
+// kStreamUnitSlots slots load together, so a unit of at most that many pieces
+// merges after one memory round trip (measured on MI355X, c4: 104.3 against
+// 105.1 us per call recomputing the stream kernel's segments from all the
+// lengths first, bit-identical); longer units read the overflow slots after.
+// Eight slots per unit: a unit of the stream split spans a few workgroups'
+// segments (c4: 2-5), and 16-wide passes loaded mostly padding (106.7-107.5
+// against 107.7-107.9 us per call). One thread per output element (GC x 128,
+// at least 256, at most 1024), so the slots load in one pass (c4, GQA 4:
+// 105.7 against 106.0 us with 256 threads and two passes, bit-identical).
 template <int GC>
 constexpr int stream_merge_threads() {
   return GC * 128 > 1024 ? 1024 : (GC * 128 > 256 ? GC * 128 : 256);
@@ -933,47 +948,65 @@ constexpr int stream_merge_threads() {
 template <int GC>
 __global__ __launch_bounds__(stream_merge_threads<GC>()) void attn_stream_merge_kernel(
     const RowsParams p) {
-  constexpr int D = 128, THREADS = stream_merge_threads<GC>();
-  __shared__ uint64_t s_part[2][THREADS / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int D = 128, THREADS = stream_merge_threads<GC>(), ROW = D + 2;
+  constexpr int C = kStreamUnitSlots;
   const uint32_t upb = p.kv_heads * p.head_chunks;
   const uint32_t unit = blockIdx.x, b = unit / upb, j = unit % upb;
-  auto visible = [&](uint32_t s) -> uint32_t { return min(p.lengths[s], p.kv_length); };
-  const uint32_t len_b = visible(b);
-  if (len_b == 0) return;  // NaN, written by the stream kernel
-  // Keys of all sequences, and of those before b (each times upb units).
-  uint64_t before = 0, total = 0;
-  for (uint32_t s = tid; s < p.batch; s += THREADS) {
-    const uint64_t n = visible(s);
-    total += n;
-    if (s < b) before += n;
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    before += __shfl_xor(before, d, 64);
-    total += __shfl_xor(total, d, 64);
-  }
-  if (lane == 0) s_part[0][wave] = before, s_part[1][wave] = total;
-  __syncthreads();
-  before = total = 0;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) before += s_part[0][w], total += s_part[1][w];
-  before *= upb;
-  total *= upb;
-  const uint64_t W = min((uint64_t)p.stream_workgroups, max((uint64_t)1, total / kStreamMinKeys));
-  const uint64_t seg = (total + W - 1) / W;
-  const uint64_t unit_start = before + (uint64_t)j * len_b;
-  const uint32_t first_wg = (uint32_t)(unit_start / seg);
-  const uint32_t last_wg = (uint32_t)((unit_start + len_b - 1) / seg);
-  if (first_wg == last_wg) return;
+  const uint32_t units = p.batch * upb;
+  const float *own = p.partial + (size_t)unit * C * GC * ROW;
+  const float *overflow = p.partial + (size_t)units * C * GC * ROW;
+  const uint32_t desc = reinterpret_cast<const uint32_t *>(
+      overflow + (size_t)(p.stream_workgroups + units) * GC * ROW)[unit];
+  const uint32_t len_b = min(p.lengths[b], p.kv_length);
   const uint32_t kvh = j / p.head_chunks, hc = j % p.head_chunks;
   uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)(kvh * p.group + hc * GC) * p.o_head;
-  // 8 pieces per pass: a unit of the stream split spans a few workgroups'
-  // segments (c4: 2-5), so 16-wide passes would load mostly padding
-  // (measured on MI355X, c4: 106.7-107.5 against 107.7-107.9 us per call,
-  // bit-identical).
-  merge_direct<D, GC, THREADS, false, 8>(p.partial + (size_t)(first_wg + unit) * GC * (D + 2),
-                                         last_wg - first_wg + 1, out, p.o_head);
+  for (int idx = threadIdx.x; idx < GC * D; idx += THREADS) {
+    const int g = idx / D, d = idx % D;
+    // Issued before the descriptor is known (the unit's own slots are in
+    // bounds whatever they hold).
+    float m[C], l[C], a[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      const float *ps = own + (size_t)(i * GC + g) * ROW;
+      m[i] = ps[0];
+      l[i] = ps[1];
+      a[i] = ps[2 + d];
+    }
+    // Zero keys: NaN, written by the stream kernel (the descriptor is stale).
+    const uint32_t pieces = desc >> 16;
+    if (len_b == 0 || pieces <= 1) return;
+    const float *base = pieces <= (uint32_t)C ? own : overflow + (size_t)((desc & 0xffff) + unit) * GC * ROW;
+    float M = -INFINITY, Ls = 0.0f, As = 0.0f;
+    for (uint32_t s0 = 0; s0 < pieces; s0 += C) {
+      if (pieces > (uint32_t)C) {
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+          const float *ps = base + (size_t)(min(s0 + i, pieces - 1) * GC + g) * ROW;
+          m[i] = ps[0];
+          l[i] = ps[1];
+          a[i] = ps[2 + d];
+        }
+      }
+      // Slots past the last piece hold other data: they take no part.
+      bool use[C];
+#pragma unroll
+      for (int i = 0; i < C; ++i) use[i] = s0 + i < pieces && m[i] != -INFINITY;
+      float cm = M;
+#pragma unroll
+      for (int i = 0; i < C; ++i) cm = use[i] ? fmaxf(cm, m[i]) : cm;
+      const float r = M == -INFINITY ? 0.0f : exp2_raw(M - cm);
+      Ls *= r;
+      As *= r;
+#pragma unroll
+      for (int i = 0; i < C; ++i) {
+        const float f = use[i] ? exp2_raw(m[i] - cm) : 0.0f;
+        Ls = use[i] ? fmaf(l[i], f, Ls) : Ls;
+        As = use[i] ? fmaf(a[i], f, As) : As;
+      }
+      M = cm;
+    }
+    out[g * p.o_head + d] = f32_to_f16(As / Ls);
+  }
 }
 
 // Merges the split partials of one (row, KV head, head chunk) unit: the

@@ -184,13 +184,23 @@ uint32_t rows_chunk(uint32_t group);
 // a stream-K split: p.stream_workgroups workgroups share the keys of all
 // sequences equally (each at least kStreamMinKeys). RowsParams as for the
 // rows kernel with tokens = 1, head_chunks = group / chunk and per-sequence
-// `lengths` (required); `partial` holds (stream_workgroups + units) * chunk
-// * (D + 2) floats. The Split phase streams the keys and writes units held
-// by one workgroup directly; the Merge phase (next on the same stream)
-// merges the pieces of the others. batch <= kStreamMaxBatch; a full 32-key
-// tile of K or V must span less than 4 GiB (32 * pos stride * 2 bytes).
+// `lengths` (required); `partial` holds stream_partial_floats(units,
+// stream_workgroups, chunk) floats: kStreamUnitSlots slots per unit, then
+// stream_workgroups + units overflow slots, each slot chunk * (D + 2)
+// floats, then one u32 descriptor per unit. The Split phase streams the
+// keys and writes units held by one workgroup directly; the first piece of
+// every unit writes its descriptor, first workgroup | pieces << 16; a
+// unit of at most kStreamUnitSlots pieces keeps piece i in its own slot i,
+// a longer one in overflow slot (workgroup + unit). The Merge phase (next
+// on the same stream) merges the pieces of split units. batch <=
+// kStreamMaxBatch; a full 32-key tile of K or V must span less than 4 GiB
+// (32 * pos stride * 2 bytes).
 constexpr uint32_t kStreamMaxBatch = 1024;
 constexpr uint32_t kStreamMinKeys = 512;
+constexpr uint32_t kStreamUnitSlots = 8;
+constexpr uint64_t stream_partial_floats(uint64_t units, uint64_t workgroups, uint32_t chunk) {
+  return (units * kStreamUnitSlots + workgroups + units) * chunk * (128 + 2) + units;
+}
 hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, RowsPhase phase,
                                 const Launch &l);
 // Head chunk of the stream kernel: the largest of 16, 8, 4, 2, 1 dividing `group`.

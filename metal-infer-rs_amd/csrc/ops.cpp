@@ -616,7 +616,7 @@ mi_status decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k
     const uint32_t workgroups = 2 * std::max<uint32_t>(batch->ctx->compute_units, 1);
     rp.group = p.G, rp.head_chunks = p.G / chunk;
     rp.stream_workgroups = workgroups;
-    const uint64_t bytes = (workgroups + units) * chunk * (uint64_t)(p.D + 2) * sizeof(float);
+    const uint64_t bytes = kernels::stream_partial_floats(units, workgroups, chunk) * sizeof(float);
     void *scratch = nullptr;
     if ((st = scratch_take(batch, src, bytes, &scratch)) != MI_OK) return st;
     rp.partial = static_cast<float *>(scratch);

@@ -389,13 +389,14 @@ def test_c4_batched_decode_seeded(ctx):
 
 
 def stream_scratch_bytes(ctx, B, hq, hkv):
-    """Scratch of a default head_dim-128 batched decode: one f32 partial
-    (max, sum, acc[128]) per workgroup (2 per CU) and unit, per head of the
-    unit's head chunk."""
+    """Scratch of a default head_dim-128 batched decode, per head of a unit's
+    head chunk one f32 partial (max, sum, acc[128]) in each of 8 fixed slots
+    per unit, one overflow slot per workgroup (2 per CU) and unit, and one
+    u32 piece descriptor per unit."""
     g = hq // hkv
     chunk = next(c for c in (16, 8, 4, 2, 1) if g % c == 0)
     units = B * hkv * (g // chunk)
-    return (2 * ctx.compute_units + units) * chunk * 130 * 4
+    return ((8 * units + 2 * ctx.compute_units + units) * chunk * 130 + units) * 4
 
 
 def _batched_case(ctx, seed, B, hq, hkv, d, cap, lengths):

@@ -104,7 +104,7 @@ def test_no_alloc_rejects_partials_beyond_its_buffer(nctx):
     """A call whose partials need more than the fixed 16 MiB fails before any
     launch, with the sizes in the message; the arena entry point runs it."""
     B, hq, hkv, d, cap = 1024, 64, 4, 128, 1
-    # stream-K: (512 workgroups + 1024 x 4 units) x 16 heads x 130 floats = 38 MB
+    # stream-K: (9 x 4096 units + 512 workgroups) x 16 heads x 130 floats = 311 MB
     rng = np.random.default_rng(9)
     q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
     kv = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
