@@ -79,9 +79,9 @@ def stats(args) -> None:
     last = args.last
     if last:
         print(f"`timed average` is over each row's last {last} dispatches, which lie in "
-              "bench.py's timed region: one replay of a graph of the workload's calls (20, or "
-              "64 for c2, which rotates 64 caches). The earlier dispatches are its eager warmup "
-              "calls and one untimed replay.\n")
+              f"bench.py's timed region: one replay of a graph of the workload's calls ({last}; "
+              "c2 rounds up to whole rotations of its 64 caches). The earlier dispatches are "
+              "the eager calls before capture and the untimed warmup replays.\n")
     print("| kernel | workgroups | calls | average (us) | timed average (us) | median (us) | "
           "min (us) | max (us) |")
     print("|---|---|---:|---:|---:|---:|---:|---:|")
