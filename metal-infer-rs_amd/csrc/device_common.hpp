@@ -175,6 +175,14 @@ __device__ __forceinline__ float load_partial(const float *ptr) {
   return __hip_atomic_load(const_cast<float *>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float2 load_partial2(const float *ptr) { return load_coherent2(ptr); }
+// Two packed words (f16 pairs) of a partial, bits unchanged.
+__device__ __forceinline__ void store_partial_words(float *ptr, uint32_t a, uint32_t b) {
+  store_coherent2(ptr, __uint_as_float(a), __uint_as_float(b));
+}
+__device__ __forceinline__ uint2 load_partial_words(const float *ptr) {
+  const float2 v = load_coherent2(ptr);
+  return make_uint2(__float_as_uint(v.x), __float_as_uint(v.y));
+}
 // Returns the counter's previous value. Call after the workgroup's partial
 // stores have completed (s_waitcnt vmcnt(0)) and it has met at a barrier.
 __device__ __forceinline__ uint32_t arrive(uint32_t *counter) {

@@ -147,12 +147,12 @@ struct PrefillParams {
   uint32_t block_m;         // packed rows per workgroup: 128, or 256 at D = 128
   float scale_log2;
   // Split-K over keys (small grids). Each split of a row tile that needs
-  // several writes its unnormalised rows (m, l, O[D]) as f32 to `partial`,
-  // laid out
+  // several writes its rows to `partial`, laid out
   // [splits][row_tiles][kv_heads][block_m / 32 waves][kPrefillPartialSlots(D)][64 lanes]
-  // float2, then counts its arrival in counters[(tile * kv_heads + kv_head)
-  // * counter_stride]; the last split to arrive merges all of them in split
-  // order and resets the counter to zero.
+  // 8-byte slots: (m, l) as f32, then O[D] / l rounded to f16, four values
+  // per slot; then counts its arrival in counters[(tile * kv_heads +
+  // kv_head) * counter_stride]; the last split to arrive merges all of them
+  // in split order and resets the counter to zero.
   float *partial;
   uint32_t *counters;
   uint32_t counter_stride;
@@ -277,9 +277,9 @@ constexpr uint32_t kPrefillBlockM2 = 256;  // large D = 128 grids
 constexpr uint32_t kPrefillBlockN = 64;
 // Most key splits of one prefill row tile.
 constexpr uint32_t kMaxPrefillSplits = 8;
-// float2 slots per lane of a split partial: (m, l), then O[D] in pairs
-// (each lane holds D / 2 values of its row).
-constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim / 4; }
+// 8-byte slots per lane of a split partial: (m, l), then O[D] / l as f16,
+// four per slot (each lane holds D / 2 values of its row).
+constexpr uint32_t kPrefillPartialSlots(uint32_t head_dim) { return 1 + head_dim / 8; }
 bool prefill_supported(uint32_t head_dim);
 // 128-row prefill workgroups resident per CU: two, or one at head_dim 256.
 constexpr uint32_t prefill_workgroups_per_cu(uint32_t head_dim) { return head_dim == 256 ? 1 : 2; }

@@ -259,8 +259,9 @@ def test_small_prefill_grids_split_the_keys():
     p = plan(q, k, k, AttentionConfig(16, 8, 128, True, 0), FLASH_PREFILL)
     assert p["grid"] == (63, 8, 1) and p["splits"] == 3 and p["block_keys"] == 11 * 64
     assert p["block_threads"] == 256
-    # (m, l) + 128 O values per row as f32, for 128 rows (4 waves) per row tile
-    assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 4) * 64 * 2 * 4
+    # per row (m, l) as f32 + 128 O values as f16 (8-byte slots of 64 lanes),
+    # for 128 rows (4 waves) per row tile
+    assert p["scratch_bytes"] == 3 * 32 * 8 * 4 * (1 + 128 // 8) * 64 * 8
     pieces, max_tiles = _pieces(2048, 2, 2048, 0, p["block_keys"])
     assert pieces == 63 and pieces * 8 <= 2 * 256
     finer = -(-max_tiles // 4) * 64  # one more split would not fit
