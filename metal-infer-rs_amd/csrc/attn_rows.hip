@@ -220,10 +220,6 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   constexpr int U = D >= 64 ? 4 : (D >= 16 ? 2 : 1);  // steps per iteration
   constexpr int THREADS = WAVES * 64;
 
-  __shared__ float s_m[WAVES][GC];
-  __shared__ float s_l[WAVES][GC];
-  __shared__ float s_acc[WAVES][GC][D];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -464,56 +460,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
   }
 
   tl.now(4);
-  // Merge the key rows of this wave (lanes that differ in their row bits).
-#pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    float M = m[g];
-#pragma unroll
-    for (int mask = LPR; mask < 64; mask <<= 1)
-      M = fmaxf(M, __shfl_xor(M, mask, 64));
-    const float f = m[g] == -INFINITY ? 0.0f : exp2_raw(m[g] - M);
-    float lw = l[g] * f;
-#pragma unroll
-    for (int mask = LPR; mask < 64; mask <<= 1) lw += __shfl_xor(lw, mask, 64);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      float a = acc[g][i] * f;
-#pragma unroll
-      for (int mask = LPR; mask < 64; mask <<= 1) a += __shfl_xor(a, mask, 64);
-      acc[g][i] = a;
-    }
-    m[g] = M;
-    l[g] = lw;
-  }
-  if (rloc == 0) {
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-      if (col == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
-      }
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) s_acc[wave][g][col * VEC + i] = acc[g][i];
-    }
-  }
-  __syncthreads();
-
-  // Merge the waves; write the output (one split) or this split's partial.
   const bool direct = nsplits == 1;
   float *part =
       p.partial + ((size_t)unit * p.max_splits + split) * GC * (D + 2);
-  for (int idx = tid; idx < GC * D; idx += THREADS) {
-    const int g = idx / D, d = idx % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
-    float L = 0.0f, A = 0.0f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      const float f = s_m[w][g] == -INFINITY ? 0.0f : exp2_raw(s_m[w][g] - M);
-      L += s_l[w][g] * f;
-      A += s_acc[w][g][d] * f;
-    }
+  // This workgroup's (M, L, A) for output element (g, d): the output itself
+  // (one split) or this split's partial.
+  auto emit = [&](int g, int d, float M, float L, float A) __attribute__((always_inline)) {
     if (direct) {
       out[g * p.o_head + d] = f32_to_f16(A / L);
     } else if constexpr (FUSED) {
@@ -528,6 +480,107 @@ __global__ __launch_bounds__(WAVES * 64) void attn_rows_kernel(
         part[g * (D + 2)] = M;
         part[g * (D + 2) + 1] = L;
       }
+    }
+  };
+  constexpr int RR = WAVES * RPW;  // key rows of the workgroup
+  if constexpr (D == 128 && GC <= 2 && RR == 32 && !STEP) {
+    // Every key row's (m, l, acc) goes to LDS as it is (32 KB); one wave
+    // turns the rows' maxima into weights 2^(m - M) and the merged sum; each
+    // output element then adds its RR rows in row order. This replaces the
+    // in-wave shuffle merge and per-thread exponentials of the general path
+    // below (measured on MI355X, c2: 7.16-7.25 against 7.27-7.33 us per
+    // call, three interleaved rounds on one box; the one-launch decode step
+    // measured 7.74 against 7.67 us with it, so it keeps the general path).
+    __shared__ float s_rm[RR][GC], s_rl[RR][GC], s_f[RR][GC], s_ml[2][GC];
+    __shared__ __attribute__((aligned(16))) float s_racc[RR][GC][D];
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      if (col == 0) {
+        s_rm[row][g] = m[g];
+        s_rl[row][g] = l[g];
+      }
+      float4 *dst = reinterpret_cast<float4 *>(&s_racc[row][g][col * VEC]);
+      dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+      dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int r = lane % RR, g = lane / RR;
+      const float mr = g < GC ? s_rm[r][g] : -INFINITY;
+      float M = mr;
+#pragma unroll
+      for (int mask = 1; mask < RR; mask <<= 1) M = fmaxf(M, __shfl_xor(M, mask, 64));
+      const float f = mr == -INFINITY ? 0.0f : exp2_raw(mr - M);
+      float lw = (g < GC ? s_rl[r][g] : 0.0f) * f;
+#pragma unroll
+      for (int mask = 1; mask < RR; mask <<= 1) lw += __shfl_xor(lw, mask, 64);
+      if (g < GC) {
+        s_f[r][g] = f;
+        if (r == 0) {
+          s_ml[0][g] = M;
+          s_ml[1][g] = lw;
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < GC * D; idx += THREADS) {
+      const int g = idx / D, d = idx % D;
+      float A = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RR; ++r) A = fmaf(s_racc[r][g][d], s_f[r][g], A);
+      emit(g, d, s_ml[0][g], s_ml[1][g], A);
+    }
+  } else {
+    __shared__ float s_m[WAVES][GC];
+    __shared__ float s_l[WAVES][GC];
+    __shared__ float s_acc[WAVES][GC][D];
+    // Merge the key rows of this wave (lanes that differ in their row bits).
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      float M = m[g];
+#pragma unroll
+      for (int mask = LPR; mask < 64; mask <<= 1)
+        M = fmaxf(M, __shfl_xor(M, mask, 64));
+      const float f = m[g] == -INFINITY ? 0.0f : exp2_raw(m[g] - M);
+      float lw = l[g] * f;
+#pragma unroll
+      for (int mask = LPR; mask < 64; mask <<= 1) lw += __shfl_xor(lw, mask, 64);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float a = acc[g][i] * f;
+#pragma unroll
+        for (int mask = LPR; mask < 64; mask <<= 1) a += __shfl_xor(a, mask, 64);
+        acc[g][i] = a;
+      }
+      m[g] = M;
+      l[g] = lw;
+    }
+    if (rloc == 0) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        if (col == 0) {
+          s_m[wave][g] = m[g];
+          s_l[wave][g] = l[g];
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) s_acc[wave][g][col * VEC + i] = acc[g][i];
+      }
+    }
+    __syncthreads();
+    // Merge the waves; write the output (one split) or this split's partial.
+    for (int idx = tid; idx < GC * D; idx += THREADS) {
+      const int g = idx / D, d = idx % D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_m[w][g]);
+      float L = 0.0f, A = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float f = s_m[w][g] == -INFINITY ? 0.0f : exp2_raw(s_m[w][g] - M);
+        L += s_l[w][g] * f;
+        A += s_acc[w][g][d] * f;
+      }
+      emit(g, d, M, L, A);
     }
   }
   if constexpr (FUSED) {
