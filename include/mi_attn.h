@@ -299,8 +299,9 @@ mi_status mi_attention_decode_batched(mi_batch *batch, const mi_tensor *q,
  * mi_attention_decode_batched, except that the split-K partials live in a
  * fixed per-GPU buffer of 16 MiB (kept until the process ends) instead of
  * the batch arena: a call whose partials need more fails with
- * MI_ERR_RESOURCE (the default head_dim-128 plan fits about 840 units of
- * one sequence, one KV head and 4 query heads), and its launches carry no
+ * MI_ERR_RESOURCE (the default head_dim-128 plan fits about 7,500 units of
+ * one sequence, one KV head and 4 query heads, in a compact partial layout
+ * past about 840 of them, with the same results), and its launches carry no
  * kernel-profiling events. Every
  * call on one GPU shares that buffer; calls in one stream's order are safe.
  * A call from a second context while the first context's last eager call is

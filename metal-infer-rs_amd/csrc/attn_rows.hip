@@ -937,12 +937,11 @@ __global__ __launch_bounds__(kStreamWaves * 64, 2) void attn_decode_stream_kerne
     // slots when it has few pieces, so that the merge launch can load them
     // with its descriptor in one round trip, else the overflow slots.
     const uint32_t units = p.batch * upb, pieces = last_wg - first_wg + 1;
-    const size_t slot = pieces <= kStreamUnitSlots
-                            ? (size_t)unit * kStreamUnitSlots + (w - first_wg)
-                            : (size_t)units * kStreamUnitSlots + w + unit;
+    const uint32_t S = p.stream_unit_slots;
+    const size_t slot = pieces <= S ? (size_t)unit * S + (w - first_wg) : (size_t)units * S + w + unit;
     float *part = p.partial + slot * GC * (D + 2);
     if (w == first_wg && tid == 0)
-      reinterpret_cast<uint32_t *>(p.partial + (size_t)units * (kStreamUnitSlots + 1) * GC * (D + 2) +
+      reinterpret_cast<uint32_t *>(p.partial + (size_t)units * (S + 1) * GC * (D + 2) +
                                    (size_t)p.stream_workgroups * GC * (D + 2))[unit] =
           first_wg | pieces << 16;
     for (int idx = tid; idx < GC * D; idx += THREADS) {
@@ -1002,12 +1001,13 @@ template <int GC>
 __global__ __launch_bounds__(stream_merge_threads<GC>()) void attn_stream_merge_kernel(
     const RowsParams p) {
   constexpr int D = 128, THREADS = stream_merge_threads<GC>(), ROW = D + 2;
-  constexpr int C = kStreamUnitSlots;
+  constexpr int C = kStreamUnitSlots;  // pieces per pass
+  const uint32_t S = p.stream_unit_slots;
   const uint32_t upb = p.kv_heads * p.head_chunks;
   const uint32_t unit = blockIdx.x, b = unit / upb, j = unit % upb;
   const uint32_t units = p.batch * upb;
-  const float *own = p.partial + (size_t)unit * C * GC * ROW;
-  const float *overflow = p.partial + (size_t)units * C * GC * ROW;
+  const float *own = p.partial + (size_t)unit * S * GC * ROW;
+  const float *overflow = p.partial + (size_t)units * S * GC * ROW;
   const uint32_t desc = reinterpret_cast<const uint32_t *>(
       overflow + (size_t)(p.stream_workgroups + units) * GC * ROW)[unit];
   const uint32_t len_b = min(p.lengths[b], p.kv_length);
@@ -1015,23 +1015,26 @@ __global__ __launch_bounds__(stream_merge_threads<GC>()) void attn_stream_merge_
   uint16_t *out = p.out + (int64_t)b * p.o_seq + (int64_t)(kvh * p.group + hc * GC) * p.o_head;
   for (int idx = threadIdx.x; idx < GC * D; idx += THREADS) {
     const int g = idx / D, d = idx % D;
-    // Issued before the descriptor is known (the unit's own slots are in
-    // bounds whatever they hold).
+    // The unit's own slots, issued before the descriptor is known (in
+    // bounds whatever they hold). The compact layout (S = 0) has none: every
+    // piece is loaded after the descriptor below.
     float m[C], l[C], a[C];
+    if (S != 0) {
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      const float *ps = own + (size_t)(i * GC + g) * ROW;
-      m[i] = ps[0];
-      l[i] = ps[1];
-      a[i] = ps[2 + d];
+      for (int i = 0; i < C; ++i) {
+        const float *ps = own + (size_t)(i * GC + g) * ROW;
+        m[i] = ps[0];
+        l[i] = ps[1];
+        a[i] = ps[2 + d];
+      }
     }
     // Zero keys: NaN, written by the stream kernel (the descriptor is stale).
     const uint32_t pieces = desc >> 16;
     if (len_b == 0 || pieces <= 1) return;
-    const float *base = pieces <= (uint32_t)C ? own : overflow + (size_t)((desc & 0xffff) + unit) * GC * ROW;
+    const float *base = pieces <= S ? own : overflow + (size_t)((desc & 0xffff) + unit) * GC * ROW;
     float M = -INFINITY, Ls = 0.0f, As = 0.0f;
     for (uint32_t s0 = 0; s0 < pieces; s0 += C) {
-      if (pieces > (uint32_t)C) {
+      if (pieces > S) {
 #pragma unroll
         for (int i = 0; i < C; ++i) {
           const float *ps = base + (size_t)(min(s0 + i, pieces - 1) * GC + g) * ROW;

@@ -68,6 +68,7 @@ struct RowsParams {
   uint32_t block_keys;      // keys per split
   uint32_t max_splits;
   uint32_t stream_workgroups;  // stream-K decode: workgroups of the launch
+  uint32_t stream_unit_slots;  // stream-K decode: fixed partial slots per unit (0 or kStreamUnitSlots)
   float scale_log2;         // rsqrt(D) * log2(e)
   // Decode step (step_k != null; one token, D = 128, 8 waves): q holds the
   // raw query rows and step_k / step_v the new token's key and value rows
@@ -185,21 +186,25 @@ uint32_t rows_chunk(uint32_t group);
 // sequences equally (each at least kStreamMinKeys). RowsParams as for the
 // rows kernel with tokens = 1, head_chunks = group / chunk and per-sequence
 // `lengths` (required); `partial` holds stream_partial_floats(units,
-// stream_workgroups, chunk) floats: kStreamUnitSlots slots per unit, then
-// stream_workgroups + units overflow slots, each slot chunk * (D + 2)
-// floats, then one u32 descriptor per unit. The Split phase streams the
-// keys and writes units held by one workgroup directly; the first piece of
-// every unit writes its descriptor, first workgroup | pieces << 16; a
-// unit of at most kStreamUnitSlots pieces keeps piece i in its own slot i,
-// a longer one in overflow slot (workgroup + unit). The Merge phase (next
-// on the same stream) merges the pieces of split units. batch <=
-// kStreamMaxBatch; a full 32-key tile of K or V must span less than 4 GiB
-// (32 * pos stride * 2 bytes).
+// stream_workgroups, chunk, stream_unit_slots) floats: stream_unit_slots
+// slots per unit, then stream_workgroups + units overflow slots, each slot
+// chunk * (D + 2) floats, then one u32 descriptor per unit. The Split phase
+// streams the keys and writes units held by one workgroup directly; the
+// first piece of every unit writes its descriptor, first workgroup |
+// pieces << 16; a unit of at most stream_unit_slots pieces keeps piece i in
+// its own slot i, a longer one in overflow slot (workgroup + unit). With
+// stream_unit_slots = 0 (the compact layout, for a fixed buffer too small
+// for the unit slots) every piece takes an overflow slot and the merge
+// loads them after the descriptor. The Merge phase (next on the same
+// stream) merges the pieces of split units, in piece order either way.
+// batch <= kStreamMaxBatch; a full 32-key tile of K or V must span less
+// than 4 GiB (32 * pos stride * 2 bytes).
 constexpr uint32_t kStreamMaxBatch = 1024;
 constexpr uint32_t kStreamMinKeys = 512;
 constexpr uint32_t kStreamUnitSlots = 8;
-constexpr uint64_t stream_partial_floats(uint64_t units, uint64_t workgroups, uint32_t chunk) {
-  return (units * kStreamUnitSlots + workgroups + units) * chunk * (128 + 2) + units;
+constexpr uint64_t stream_partial_floats(uint64_t units, uint64_t workgroups, uint32_t chunk,
+                                         uint32_t unit_slots) {
+  return (units * unit_slots + workgroups + units) * chunk * (128 + 2) + units;
 }
 hipError_t launch_decode_stream(const RowsParams &p, uint32_t chunk, RowsPhase phase,
                                 const Launch &l);

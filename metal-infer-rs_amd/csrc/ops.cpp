@@ -616,7 +616,16 @@ mi_status decode_batched(mi_batch *batch, const mi_tensor *q, const mi_tensor *k
     const uint32_t workgroups = 2 * std::max<uint32_t>(batch->ctx->compute_units, 1);
     rp.group = p.G, rp.head_chunks = p.G / chunk;
     rp.stream_workgroups = workgroups;
-    const uint64_t bytes = kernels::stream_partial_floats(units, workgroups, chunk) * sizeof(float);
+    // Fixed slots per unit, so that the merge loads a unit's pieces with its
+    // descriptor; a fixed buffer too small for them takes the compact layout
+    // (every piece in an overflow slot, same merge order and results).
+    uint32_t unit_slots = kernels::kStreamUnitSlots;
+    uint64_t bytes = kernels::stream_partial_floats(units, workgroups, chunk, unit_slots) * sizeof(float);
+    if (src.fixed != nullptr && bytes > src.limit) {
+      unit_slots = 0;
+      bytes = kernels::stream_partial_floats(units, workgroups, chunk, 0) * sizeof(float);
+    }
+    rp.stream_unit_slots = unit_slots;
     void *scratch = nullptr;
     if ((st = scratch_take(batch, src, bytes, &scratch)) != MI_OK) return st;
     rp.partial = static_cast<float *>(scratch);

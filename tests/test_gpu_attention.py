@@ -388,15 +388,19 @@ def test_c4_batched_decode_seeded(ctx):
         print(f"c4 block={block}: max-abs {worst:.2e}")
 
 
-def stream_scratch_bytes(ctx, B, hq, hkv):
-    """Scratch of a default head_dim-128 batched decode, per head of a unit's
-    head chunk one f32 partial (max, sum, acc[128]) in each of 8 fixed slots
-    per unit, one overflow slot per workgroup (2 per CU) and unit, and one
-    u32 piece descriptor per unit."""
+def stream_scratch_bytes(ctx, B, hq, hkv, limit=16 << 20):
+    """Scratch of a default head_dim-128 batched decode in a buffer of
+    `limit` bytes: per head of a unit's head chunk one f32 partial (max, sum,
+    acc[128]) in each of 8 fixed slots per unit, one overflow slot per
+    workgroup (2 per CU) and unit, and one u32 piece descriptor per unit; or,
+    when that exceeds the buffer, the compact layout without the fixed
+    slots."""
     g = hq // hkv
     chunk = next(c for c in (16, 8, 4, 2, 1) if g % c == 0)
     units = B * hkv * (g // chunk)
-    return ((8 * units + 2 * ctx.compute_units + units) * chunk * 130 + units) * 4
+    fixed = ((8 * units + 2 * ctx.compute_units + units) * chunk * 130 + units) * 4
+    compact = ((2 * ctx.compute_units + units) * chunk * 130 + units) * 4
+    return fixed if fixed <= limit else compact
 
 
 def _batched_case(ctx, seed, B, hq, hkv, d, cap, lengths):

@@ -100,11 +100,40 @@ def test_no_alloc_matches_the_arena_entry_point_on_two_calls(nctx, block):
     kt.free(), vt.free()
 
 
+def test_no_alloc_compact_layout_when_unit_slots_do_not_fit(nctx):
+    """128 sequences x 8 KV heads (1024 units of 4 query heads): the fixed 8
+    slots per unit would need 20 MB, so the no-allocation call takes the
+    compact layout (every piece in an overflow slot, 3.2 MB). Bit-identical
+    to the arena entry point (fixed slots, same merge order) on two calls,
+    and within 2e-3 of the oracle on sampled sequences."""
+    B, hq, hkv, d, cap = 128, 32, 8, 128, 600
+    rng = np.random.default_rng(11)
+    lengths = [int(x) for x in rng.integers(1, cap + 1, B)]
+    lengths[5] = 0
+    q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
+    k = [rng.standard_normal((cap, hkv, d)).astype(np.float16).view(np.uint16) for _ in range(B)]
+    v = [rng.standard_normal((cap, hkv, d)).astype(np.float16).view(np.uint16) for _ in range(B)]
+    kt, vt, kview, vview = _cache(nctx, k, v, lengths, cap)
+    cfg = mi_attn.AttentionConfig(hq, hkv, d, True, 0)
+    for rep in range(2):
+        ref, got = _both(nctx, q, kview, vview, lengths, cfg, 0)
+        assert (got.view(np.uint16) == ref.view(np.uint16)).all(), f"call {rep} differs"
+    for b in (0, 5, 37, 127):
+        n = lengths[b]
+        if n == 0:
+            assert np.isnan(got[b].view(np.float16).astype(np.float32)).all()
+            continue
+        oracle = oracle_attention(q[b:b + 1], k[b][:n], v[b][:n], hq=hq, hkv=hkv, d=d, off=n - 1)
+        assert_parity(got[b:b + 1], oracle, label=f"compact seq {b}")
+    kt.free(), vt.free()
+
+
 def test_no_alloc_rejects_partials_beyond_its_buffer(nctx):
     """A call whose partials need more than the fixed 16 MiB fails before any
     launch, with the sizes in the message; the arena entry point runs it."""
     B, hq, hkv, d, cap = 1024, 64, 4, 128, 1
-    # stream-K: (9 x 4096 units + 512 workgroups) x 16 heads x 130 floats = 311 MB
+    # stream-K: (512 workgroups + 4096 units) x 16 heads x 130 floats = 38 MB, even
+    # in the compact layout (no fixed slots per unit)
     rng = np.random.default_rng(9)
     q = rng.standard_normal((B, hq, d)).astype(np.float16).view(np.uint16)
     kv = rng.standard_normal((B, cap, hkv, d)).astype(np.float16).view(np.uint16)
